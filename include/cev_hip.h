@@ -1,0 +1,229 @@
+/*
+ * cev_hip.h -- C ABI of the MI355X (gfx950) packed-prefill attention path.
+ *
+ * The library (libcev_hip.so) replaces the tensor ops under the reference's
+ * attention call: the QK-norm + RoPE prologue of Attention::forward and the
+ * matmul -> softmax -> matmul core of Attention::attend, with the dense
+ * additive mask replaced by a block-offset table.  Reference sites (paths
+ * relative to the reference checkout):
+ *   crates/cev-model/src/qwen3.rs:187-220   Qwen3 Attention::forward / attend
+ *   crates/cev-model/src/qwen35.rs:526-579  Qwen3.5 gated Attention::forward / attend
+ *   crates/cev-model/src/engine.rs:389-442  the packed pass's dense mask
+ *   crates/cev-model/src/qwen3.rs:153-169   segment_mask (chunked prefill)
+ *   crates/cev-model/src/qwen35.rs:469-498  branch_mask / bidirectional_mask
+ *
+ * Conventions
+ *   - Every entry point returns an int32 status: CEV_OK (0) or a negative
+ *     CEV_ERR_*; cev_last_error() gives a thread-local message.  Nothing
+ *     throws across the ABI.
+ *   - Device pointers are caller-owned, borrowed for the stream-ordered
+ *     launch and never retained.  Launchers allocate nothing.
+ *   - Host functions (no stream argument) touch no GPU state.
+ *   - Launchers keep no mutable global state: calls on distinct streams may
+ *     run concurrently from several threads.
+ *   - A stream is a hipStream_t passed as an opaque pointer (NULL = default).
+ */
+#ifndef CEV_HIP_H
+#define CEV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CEV_ABI_VERSION 1
+
+enum {
+  CEV_OK = 0,
+  CEV_ERR_INVALID = -1,     /* malformed argument, table or plan            */
+  CEV_ERR_UNSUPPORTED = -2, /* a shape or dtype the kernels do not cover     */
+  CEV_ERR_HIP = -3,         /* a HIP runtime error                           */
+  CEV_ERR_SPACE = -4        /* caller buffer too small (see *_size)          */
+};
+
+enum { CEV_F32 = 0, CEV_BF16 = 1 };
+
+#define CEV_MAX_SPANS 4
+
+typedef void* cev_stream;
+
+/* ------------------------------------------------------------------ */
+/* Block-offset table.
+ *
+ * Keys live in one index space: [0, s_cache) are cached keys (the prefix
+ * K/V, several plans' pasts concatenated as engine.rs:367-387 does), and
+ * [s_cache, s_cache + t) are the keys of the t new tokens of this call.
+ * A block is a run of packed query rows [q_begin, q_begin + q_len).  Row j
+ * of the block (0-based) sees:
+ *   - every key of every span (fully visible key ranges: the plan's past,
+ *     the plan's prefix tail for question tokens);
+ *   - causal != 0: local keys [local_begin, local_begin + j];
+ *   - causal == 0 (bidirectional): local keys [local_begin, local_begin +
+ *     valid_len), and a padded row (j >= valid_len) also its own key
+ *     local_begin + j, so it never attends to nothing (qwen35.rs:491-494).
+ * This expresses engine.rs:418-442, qwen3.rs:157-169 and qwen35.rs:469-498.
+ * Spans must be disjoint from each other and from the block's own local
+ * keys; blocks must not overlap.  Rows outside every block are left
+ * untouched in the output. */
+typedef struct {
+  int32_t begin; /* first key (global key index) */
+  int32_t len;   /* number of keys, >= 0        */
+} cev_span;
+
+typedef struct {
+  int32_t q_begin;
+  int32_t q_len;       /* >= 1 */
+  int32_t valid_len;   /* bidirectional: real rows (0..q_len); causal: q_len */
+  int32_t causal;      /* 1 causal, 0 bidirectional */
+  int32_t local_begin; /* global key index of the block's own first token */
+  int32_t n_spans;     /* 0..CEV_MAX_SPANS */
+  cev_span spans[CEV_MAX_SPANS];
+} cev_block;
+
+/* ------------------------------------------------------------------ */
+/* Attention descriptor.  Strides are in elements.  Shapes (reference
+ * layout in brackets):
+ *   q       (t, hq, d)          element (i, h, e) at q[i*q_stride_t + h*q_stride_h + e]
+ *                               [(1, hq, t, d) in qwen3.rs:193]
+ *   k/v_cache (hkv, s_cache, d) at (h, j, e): [h*kc_stride_h + j*kc_stride_s + e]
+ *   k/v_new (t, hkv, d)         at (i, h, e): [i*kn_stride_t + h*kn_stride_h + e]
+ *                               [the cat of qwen3.rs:197-200 is not needed]
+ *   gate    (t, hq, d)          optional sigmoid gate (qwen35.rs:556-558)
+ *   out     (t, hq, d)          [(1, hq, t, d) transposed for o_proj, qwen3.rs:202]
+ * head h reads kv head h / (hq / hkv) (repeat_kv, qwen3.rs:145-151).
+ * scale is applied to q.k before the softmax (reference: 1/sqrt(d) as f32,
+ * qwen3.rs:207). */
+typedef struct {
+  int32_t dtype;      /* CEV_F32 or CEV_BF16: q, k, v, gate, out */
+  int32_t n_q_heads;  /* hq */
+  int32_t n_kv_heads; /* hkv, divides hq, hq/hkv <= 8 */
+  int32_t head_dim;   /* 128 or 256 (f32: 128) */
+  int32_t t;          /* packed new tokens = query rows */
+  int32_t s_cache;    /* cached keys before the new tokens */
+  float scale;
+  int32_t has_gate;
+  int64_t q_stride_t, q_stride_h;
+  int64_t kc_stride_s, kc_stride_h;
+  int64_t vc_stride_s, vc_stride_h;
+  int64_t kn_stride_t, kn_stride_h;
+  int64_t vn_stride_t, vn_stride_h;
+  int64_t g_stride_t, g_stride_h;
+  int64_t o_stride_t, o_stride_h;
+} cev_attn_desc;
+
+/* Fills `d` with dense strides for the layouts above (token-major q, gate,
+ * out; head-major cache; token-major new K/V), scale = 1/sqrt(head_dim). */
+int32_t cev_attn_desc_init(cev_attn_desc* d, int32_t dtype, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t t,
+                           int32_t s_cache, int32_t has_gate);
+
+/* ------------------------------------------------------------------ */
+/* Attention plan: the table compiled into work tiles (host only).
+ * cev_attn_plan_size reports the bytes cev_attn_plan_build writes; both
+ * validate the descriptor and the table and fail before anything runs.
+ * The caller copies the plan to device memory (any copy API) and passes
+ * both copies to cev_packed_attention: the host copy is read for
+ * validation and the grid size, the device copy by the kernel. */
+int32_t cev_attn_plan_size(const cev_attn_desc* d, const cev_block* blocks, int32_t n_blocks, size_t* bytes);
+int32_t cev_attn_plan_build(const cev_attn_desc* d, const cev_block* blocks, int32_t n_blocks, void* plan, size_t bytes);
+
+/* Packed-prefill attention: replaces Attention::attend
+ * (qwen3.rs:206-220, qwen35.rs:563-579) plus the output gate of
+ * qwen35.rs:556-558 when has_gate.  k_cache/v_cache may be NULL when
+ * s_cache == 0, gate NULL when !has_gate. */
+int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q, const void* k_cache,
+                             const void* v_cache, const void* k_new, const void* v_new, const void* gate, void* out, cev_stream stream);
+
+/* ------------------------------------------------------------------ */
+/* Fused QK RMSNorm + RoPE with per-token positions: replaces
+ * q_norm / k_norm + Rotary::apply of qwen3.rs:193-196 and the Qwen3.5 form
+ * of qwen35.rs:529-539 (weight 1 + w, partial rotary, [q | gate] heads).
+ *   q_in  (t, hq, d)  at q_in[i*qi_stride_t + h*qi_stride_h + e]   (gated q_proj: qi_stride_h = 2d)
+ *   k_in  (t, hkv, d) at k_in[i*ki_stride_t + h*ki_stride_h + e]
+ *   q_out, k_out likewise with qo_* / ko_* strides (k_out may point into
+ *   the K/V cache).  pos (t) int32 positions; cos/sin (n_pos, rotary_dim/2)
+ *   in the model dtype as built by cev_rope_table. */
+typedef struct {
+  int32_t dtype;
+  int32_t n_q_heads, n_kv_heads, head_dim;
+  int32_t t;
+  int32_t rotary_dim;   /* even, <= head_dim */
+  int32_t n_pos;        /* rows of the cos/sin table */
+  int32_t weight_plus_one; /* 0: x*w (Qwen3); 1: x*(1+w) (Qwen3.5) */
+  float eps;
+  int64_t qi_stride_t, qi_stride_h;
+  int64_t ki_stride_t, ki_stride_h;
+  int64_t qo_stride_t, qo_stride_h;
+  int64_t ko_stride_t, ko_stride_h;
+} cev_qknorm_desc;
+
+int32_t cev_qknorm_desc_init(cev_qknorm_desc* d, int32_t dtype, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t t,
+                             int32_t rotary_dim, int32_t n_pos, int32_t weight_plus_one, float eps, int32_t gated_q);
+
+int32_t cev_qknorm_rope(const cev_qknorm_desc* d, const void* q_in, const void* k_in, const void* w_q, const void* w_k, const int32_t* pos,
+                        const void* cos, const void* sin, void* q_out, void* k_out, cev_stream stream);
+
+/* RoPE cos/sin table exactly as Rotary::new builds it (qwen3.rs:107-118):
+ * inv_i = 1 / (theta^(2i/rotary_dim) in f64, rounded to f32), angle =
+ * f32(p) * inv_i in f32, cos/sin in f32, then rounded to dtype.  Host only;
+ * cos/sin are (n_pos, rotary_dim/2) arrays of f32 or bf16 (uint16 bits). */
+int32_t cev_rope_table(double theta, int32_t rotary_dim, int32_t n_pos, int32_t dtype, void* cos, void* sin);
+
+/* ------------------------------------------------------------------ */
+/* Table builders (host only). */
+
+/* The packed pass of engine.rs:365-442.  Plans p = 0..n_plans-1 in plan
+ * order carry past_len[p] computed tokens (stored in the cache at the plan
+ * order concatenation offset), prefix_len[p] and tail_start[p] (the first
+ * prefix token not yet computed; == prefix_len[p] means no tail).  Items
+ * k = 0..n_items-1 are questions (item_plan[k], item_len[k]).  Writes one
+ * block per tail and per question (tails first, in plan order, then
+ * questions in item order, as the reference packs tokens), pos[n] with the
+ * per-question RoPE restart at prefix_len (engine.rs:411) and gather[k]
+ * (engine.rs:415).  *n_tokens / *n_out_blocks receive the counts; with
+ * NULL outputs only the counts are computed. */
+int32_t cev_table_from_plans(int32_t n_plans, const int32_t* past_len, const int32_t* prefix_len, const int32_t* tail_start, int32_t n_items,
+                             const int32_t* item_plan, const int32_t* item_len, cev_block* blocks, int32_t max_blocks, int32_t* n_out_blocks,
+                             int32_t* pos, int32_t max_tokens, int32_t* n_tokens, int32_t* gather);
+
+/* Rows of a batch (HybridEngine::rows, hybrid.rs:592-617): b rows of t
+ * tokens packed row-major.  causal != 0: each row continues `past` cached
+ * keys (branch_mask, qwen35.rs:471-479); causal == 0: no cache, row r has
+ * lengths[r] real tokens (bidirectional_mask, qwen35.rs:483-498). */
+int32_t cev_table_from_rows(int32_t b, int32_t t, int32_t past, int32_t causal, const int32_t* lengths, cev_block* blocks, int32_t max_blocks);
+
+/* segment_mask of qwen3.rs:157-169 for contiguous segments: n new tokens
+ * after `past` cached ones, seg[i] their segment ids.  A segment id that
+ * reappears after another one is rejected (CEV_ERR_UNSUPPORTED). */
+int32_t cev_table_from_segment_ids(const uint32_t* seg, int32_t n, int32_t past, cev_block* blocks, int32_t max_blocks, int32_t* n_out_blocks);
+
+/* Expands a table into the dense additive mask (t, s_cache + t) of 0 and
+ * -inf, for validation against the reference mask. */
+int32_t cev_table_to_dense_mask(const cev_block* blocks, int32_t n_blocks, int32_t t, int32_t s_cache, float* mask);
+
+/* Recovers a table from a dense additive mask (t, s_cache + t): row i's
+ * local run is the visible run holding its own key s_cache + i (or, for a
+ * padded bidirectional row, the run before it); consecutive rows with equal
+ * spans and a compatible local run form one block.  Fails with
+ * CEV_ERR_UNSUPPORTED on patterns a table cannot express. */
+int32_t cev_table_from_dense_mask(const float* mask, int32_t t, int32_t s_cache, cev_block* blocks, int32_t max_blocks, int32_t* n_out_blocks);
+
+/* ------------------------------------------------------------------ */
+/* Runtime helpers for hosts without a HIP binding (the Rust host). */
+const char* cev_last_error(void);
+int32_t cev_abi_version(void);
+int32_t cev_device_info(int32_t device, char* name, size_t name_len, int32_t* n_cus, int64_t* hbm_bytes, int32_t* clock_mhz);
+int32_t cev_malloc(void** ptr, size_t bytes);
+int32_t cev_free(void* ptr);
+int32_t cev_memcpy_h2d(void* dst, const void* src, size_t bytes, cev_stream stream);
+int32_t cev_memcpy_d2h(void* dst, const void* src, size_t bytes, cev_stream stream);
+int32_t cev_stream_create(cev_stream* stream);
+int32_t cev_stream_destroy(cev_stream stream);
+int32_t cev_stream_synchronize(cev_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CEV_HIP_H */

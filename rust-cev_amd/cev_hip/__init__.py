@@ -1,0 +1,314 @@
+"""Host side of the MI355X packed-prefill attention path, over libcev_hip.so.
+
+This mirrors what the reference's attention call needs from its tensor layer
+(crates/cev-model/src/qwen3.rs:187-220, crates/cev-model/src/qwen35.rs:526-579)
+with the block-offset table in place of the dense mask builders
+(crates/cev-model/src/engine.rs:389-442, qwen3.rs:153-169, qwen35.rs:469-498).
+Every compute call goes through the C ABI; torch is used only to hold device
+memory and to name the current stream.  There is no CPU fallback: without the
+built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import synth  # noqa: F401  (re-exported)
+from ._abi import (CEV_BF16, CEV_F32, CEV_MAX_SPANS, AttnDesc, Block, CevError, QkNormDesc, Span, check, lib)
+
+__all__ = [
+    "CEV_BF16", "CEV_F32", "CevError", "Block", "Span", "BlockTable", "AttnPlan", "PackedAttention",
+    "packed_attention", "qknorm_rope", "rope_table", "Rotary", "device_info", "synth",
+]
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dtype_code(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.float32:
+        return CEV_F32
+    if t.dtype == torch.bfloat16:
+        return CEV_BF16
+    raise CevError(-2, f"dtype {t.dtype} not supported (float32, bfloat16)")
+
+
+def _stream_ptr(stream):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+# ---------------------------------------------------------------------------
+# Block-offset table
+
+
+class BlockTable:
+    """A list of cev_block rows: which keys each packed query row sees."""
+
+    def __init__(self, blocks: Sequence[Block], t: int, s_cache: int):
+        self.blocks = list(blocks)
+        self.t = int(t)
+        self.s_cache = int(s_cache)
+
+    def __len__(self):
+        return len(self.blocks)
+
+    def array(self):
+        arr = (Block * max(1, len(self.blocks)))()
+        for i, b in enumerate(self.blocks):
+            arr[i] = b
+        return arr
+
+    @staticmethod
+    def block(q_begin, q_len, local_begin, spans=(), causal=True, valid_len=None) -> Block:
+        b = Block()
+        b.q_begin, b.q_len, b.local_begin = int(q_begin), int(q_len), int(local_begin)
+        b.causal = 1 if causal else 0
+        b.valid_len = int(q_len if valid_len is None else valid_len)
+        if len(spans) > CEV_MAX_SPANS:
+            raise CevError(-1, f"{len(spans)} spans > {CEV_MAX_SPANS}")
+        b.n_spans = len(spans)
+        for i, (s0, sl) in enumerate(spans):
+            b.spans[i] = Span(int(s0), int(sl))
+        return b
+
+    @classmethod
+    def from_plans(cls, plans, items):
+        """engine.rs:365-442.  plans: [(past_len, prefix_len, tail_start)];
+        items: [(plan, question_len)].  Returns (table, pos, gather)."""
+        L = lib()
+        n_pl = len(plans)
+        a = lambda xs: (C.c_int32 * max(1, len(xs)))(*[int(x) for x in xs])  # noqa: E731
+        past, pre, ts = a([p[0] for p in plans]), a([p[1] for p in plans]), a([p[2] for p in plans])
+        ip, il = a([i[0] for i in items]), a([i[1] for i in items])
+        nb, nt = C.c_int32(), C.c_int32()
+        check(L.cev_table_from_plans(n_pl, past, pre, ts, len(items), ip, il, None, 0, C.byref(nb), None, 0, C.byref(nt), None))
+        blocks = (Block * max(1, nb.value))()
+        pos = (C.c_int32 * max(1, nt.value))()
+        gather = (C.c_int32 * max(1, len(items)))()
+        check(L.cev_table_from_plans(n_pl, past, pre, ts, len(items), ip, il, blocks, nb.value, C.byref(nb), pos, nt.value,
+                                     C.byref(nt), gather))
+        s_cache = int(sum(p[0] for p in plans))
+        tab = cls([blocks[i] for i in range(nb.value)], nt.value, s_cache)
+        return tab, np.frombuffer(pos, np.int32)[: nt.value].copy(), np.frombuffer(gather, np.int32)[: len(items)].copy()
+
+    @classmethod
+    def from_rows(cls, b: int, t: int, past: int = 0, causal: bool = True, lengths=None):
+        """HybridEngine::rows (hybrid.rs:592-617): b rows of t tokens."""
+        blocks = (Block * max(1, b))()
+        ln = None if lengths is None else (C.c_int32 * max(1, b))(*[int(x) for x in lengths])
+        check(lib().cev_table_from_rows(b, t, past, 1 if causal else 0, ln, blocks, b))
+        return cls([blocks[i] for i in range(b)], b * t, past)
+
+    @classmethod
+    def from_segment_ids(cls, seg, past: int = 0):
+        """segment_mask (qwen3.rs:157-169) for contiguous segments."""
+        seg = np.ascontiguousarray(seg, np.uint32)
+        n = seg.size
+        nb = C.c_int32()
+        sp = seg.ctypes.data_as(C.POINTER(C.c_uint32))
+        check(lib().cev_table_from_segment_ids(sp, n, past, None, 0, C.byref(nb)))
+        blocks = (Block * max(1, nb.value))()
+        check(lib().cev_table_from_segment_ids(sp, n, past, blocks, nb.value, C.byref(nb)))
+        return cls([blocks[i] for i in range(nb.value)], n, past)
+
+    @classmethod
+    def from_dense_mask(cls, mask: np.ndarray, s_cache: int):
+        mask = np.ascontiguousarray(mask, np.float32)
+        t = mask.shape[0]
+        assert mask.shape == (t, s_cache + t)
+        nb = C.c_int32()
+        check(lib().cev_table_from_dense_mask(C.c_void_p(mask.ctypes.data), t, s_cache, None, 0, C.byref(nb)))
+        blocks = (Block * max(1, nb.value))()
+        check(lib().cev_table_from_dense_mask(C.c_void_p(mask.ctypes.data), t, s_cache, blocks, nb.value, C.byref(nb)))
+        return cls([blocks[i] for i in range(nb.value)], t, s_cache)
+
+    def to_dense_mask(self) -> np.ndarray:
+        m = np.empty((self.t, self.s_cache + self.t), np.float32)
+        check(lib().cev_table_to_dense_mask(self.array(), len(self.blocks), self.t, self.s_cache, C.c_void_p(m.ctypes.data)))
+        return m
+
+
+# ---------------------------------------------------------------------------
+# Attention
+
+
+def attn_desc(dtype: int, hq: int, hkv: int, d: int, t: int, s_cache: int, has_gate: bool = False, scale: Optional[float] = None,
+              **strides) -> AttnDesc:
+    desc = AttnDesc()
+    check(lib().cev_attn_desc_init(C.byref(desc), dtype, hq, hkv, d, t, s_cache, 1 if has_gate else 0))
+    if scale is not None:
+        desc.scale = float(scale)
+    for k, v in strides.items():
+        setattr(desc, k, int(v))
+    return desc
+
+
+class AttnPlan:
+    """A table compiled for one descriptor: host bytes plus a device copy."""
+
+    def __init__(self, desc: AttnDesc, table: BlockTable, device=None):
+        L = lib()
+        arr = table.array()
+        size = C.c_size_t()
+        check(L.cev_attn_plan_size(C.byref(desc), arr, len(table), C.byref(size)))
+        raw = np.zeros(size.value + 16, np.uint8)
+        off = (-raw.ctypes.data) % 16
+        self.host = raw[off: off + size.value]
+        check(L.cev_attn_plan_build(C.byref(desc), arr, len(table), C.c_void_p(self.host.ctypes.data), size.value))
+        hdr = self.host[:64].view(np.int32)
+        self.n_tiles = int(hdr[2])
+        self.n_segs = int(hdr[3])
+        self.tile_rows = int(hdr[6])
+        self.nbytes = size.value
+        self.dev = None
+        if device is not None:
+            torch = _torch()
+            self.dev = torch.from_numpy(self.host.copy()).to(device)
+
+    def tiles(self) -> np.ndarray:
+        hdr = self.host[:64].view(np.int32)
+        return self.host.view(np.int32)[hdr[11]: hdr[11] + 4 * self.n_tiles].reshape(-1, 4)
+
+    def segs(self) -> np.ndarray:
+        hdr = self.host[:64].view(np.int32)
+        return self.host.view(np.int32)[hdr[12]: hdr[12] + 4 * self.n_segs].reshape(-1, 4)
+
+
+class PackedAttention:
+    """Packed-prefill attention over fixed shapes: Attention::attend
+    (qwen3.rs:206-220) with K/V given as (cache, new) and a block table.
+
+    Layouts: q, gate, out (t, hq, d) (any strides with unit last stride);
+    k_cache / v_cache (hkv, s_cache, d); k_new / v_new (t, hkv, d)."""
+
+    def __init__(self, q, k_new, table: BlockTable, k_cache=None, s_cache: int = 0, has_gate: bool = False,
+                 scale: Optional[float] = None, out=None, gate=None, v_new=None, v_cache=None):
+        t, hq, d = q.shape
+        hkv = k_new.shape[1]
+        if table.t != t or table.s_cache != s_cache:
+            raise CevError(-1, f"table is for t={table.t}, s_cache={table.s_cache}; call has t={t}, s_cache={s_cache}")
+        self.dtype = _dtype_code(q)
+        self.desc = attn_desc(self.dtype, hq, hkv, d, t, s_cache, has_gate, scale)
+        self._set_strides(q, k_new, v_new if v_new is not None else k_new, k_cache, v_cache if v_cache is not None else k_cache,
+                          out if out is not None else q, gate)
+        self.plan = AttnPlan(self.desc, table, device=q.device)
+
+    def _set_strides(self, q, kn, vn, kc, vc, out, gate):
+        D = self.desc
+        for t_ in (q, kn, vn, kc, vc, out, gate):
+            if t_ is not None and t_.stride(-1) != 1:
+                raise CevError(-2, "last dimension must be contiguous")
+        D.q_stride_t, D.q_stride_h = q.stride(0), q.stride(1)
+        D.kn_stride_t, D.kn_stride_h = kn.stride(0), kn.stride(1)
+        D.vn_stride_t, D.vn_stride_h = vn.stride(0), vn.stride(1)
+        if kc is not None:
+            D.kc_stride_h, D.kc_stride_s = kc.stride(0), kc.stride(1)
+            D.vc_stride_h, D.vc_stride_s = vc.stride(0), vc.stride(1)
+        D.o_stride_t, D.o_stride_h = out.stride(0), out.stride(1)
+        if gate is not None:
+            D.g_stride_t, D.g_stride_h = gate.stride(0), gate.stride(1)
+
+    def __call__(self, q, k_new, v_new, k_cache=None, v_cache=None, gate=None, out=None, stream=None):
+        torch = _torch()
+        if out is None:
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        self._set_strides(q, k_new, v_new, k_cache, v_cache, out, gate)
+        check(lib().cev_packed_attention(C.byref(self.desc), C.c_void_p(self.plan.host.ctypes.data), _ptr(self.plan.dev), _ptr(q),
+                                         _ptr(k_cache), _ptr(v_cache), _ptr(k_new), _ptr(v_new), _ptr(gate), _ptr(out),
+                                         _stream_ptr(stream)))
+        return out
+
+
+def packed_attention(q, k_new, v_new, table: BlockTable, k_cache=None, v_cache=None, gate=None, scale=None, out=None, stream=None):
+    s_cache = 0 if k_cache is None else k_cache.shape[1]
+    op = PackedAttention(q, k_new, table, k_cache=k_cache, s_cache=s_cache, has_gate=gate is not None, scale=scale, out=out,
+                         gate=gate, v_new=v_new, v_cache=v_cache)
+    return op(q, k_new, v_new, k_cache, v_cache, gate, out, stream)
+
+
+# ---------------------------------------------------------------------------
+# QK-norm + RoPE
+
+
+def rope_table(theta: float, rotary_dim: int, n_pos: int, dtype: int):
+    """Rotary::new (qwen3.rs:107-118) on the host: (cos, sin) as numpy
+    arrays (n_pos, rotary_dim/2), float32 or uint16 bf16 bits."""
+    half = rotary_dim // 2
+    npdt = np.float32 if dtype == CEV_F32 else np.uint16
+    c = np.empty((n_pos, half), npdt)
+    s = np.empty((n_pos, half), npdt)
+    check(lib().cev_rope_table(float(theta), int(rotary_dim), int(n_pos), int(dtype), C.c_void_p(c.ctypes.data),
+                               C.c_void_p(s.ctypes.data)))
+    return c, s
+
+
+class Rotary:
+    """Device-resident cos/sin table in the model dtype."""
+
+    def __init__(self, theta: float, rotary_dim: int, n_pos: int, dtype, device):
+        torch = _torch()
+        code = CEV_F32 if dtype == torch.float32 else CEV_BF16
+        c, s = rope_table(theta, rotary_dim, n_pos, code)
+        if code == CEV_BF16:
+            c = torch.from_numpy(c.view(np.int16)).view(torch.bfloat16)
+            s = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16)
+        else:
+            c, s = torch.from_numpy(c), torch.from_numpy(s)
+        self.cos = c.to(device)
+        self.sin = s.to(device)
+        self.rotary_dim = rotary_dim
+        self.n_pos = n_pos
+
+
+def qknorm_rope(q_in, k_in, w_q, w_k, pos, rot: Rotary, eps: float, plus_one: bool = False, q_out=None, k_out=None, stream=None):
+    """RMSNorm + RoPE of q (t, hq, d) and k (t, hkv, d) views (qwen3.rs:193-196,
+    qwen35.rs:529-539).  q_in may be a strided view of a gated q_proj output."""
+    torch = _torch()
+    t, hq, d = q_in.shape
+    hkv = k_in.shape[1]
+    code = _dtype_code(q_in)
+    if q_out is None:
+        q_out = torch.empty((t, hq, d), dtype=q_in.dtype, device=q_in.device)
+    if k_out is None:
+        k_out = torch.empty((t, hkv, d), dtype=k_in.dtype, device=k_in.device)
+    desc = QkNormDesc()
+    check(lib().cev_qknorm_desc_init(C.byref(desc), code, hq, hkv, d, t, rot.rotary_dim, rot.n_pos, 1 if plus_one else 0, float(eps), 0))
+    for t_ in (q_in, k_in, q_out, k_out):
+        if t_.stride(-1) != 1:
+            raise CevError(-2, "last dimension must be contiguous")
+    desc.qi_stride_t, desc.qi_stride_h = q_in.stride(0), q_in.stride(1)
+    desc.ki_stride_t, desc.ki_stride_h = k_in.stride(0), k_in.stride(1)
+    desc.qo_stride_t, desc.qo_stride_h = q_out.stride(0), q_out.stride(1)
+    desc.ko_stride_t, desc.ko_stride_h = k_out.stride(0), k_out.stride(1)
+    if pos.dtype != torch.int32:
+        raise CevError(-1, "positions must be int32")
+    check(lib().cev_qknorm_rope(C.byref(desc), _ptr(q_in), _ptr(k_in), _ptr(w_q), _ptr(w_k), _ptr(pos), _ptr(rot.cos), _ptr(rot.sin),
+                                _ptr(q_out), _ptr(k_out), _stream_ptr(stream)))
+    return q_out, k_out
+
+
+@dataclass
+class DeviceInfo:
+    name: str
+    n_cus: int
+    hbm_bytes: int
+    clock_mhz: int
+
+
+def device_info(device: int = 0) -> DeviceInfo:
+    name = C.create_string_buffer(128)
+    cus, hbm, clk = C.c_int32(), C.c_int64(), C.c_int32()
+    check(lib().cev_device_info(device, name, 128, C.byref(cus), C.byref(hbm), C.byref(clk)))
+    return DeviceInfo(name.value.decode(), cus.value, hbm.value, clk.value)

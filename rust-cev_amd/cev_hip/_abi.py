@@ -1,0 +1,133 @@
+"""ctypes view of include/cev_hip.h (libcev_hip.so).
+
+Struct layouts and signatures mirror the header one to one; a Rust host
+binds the same symbols with `extern "C"` declarations.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "build", "libcev_hip.so")
+
+CEV_OK = 0
+CEV_ERR_INVALID = -1
+CEV_ERR_UNSUPPORTED = -2
+CEV_ERR_HIP = -3
+CEV_ERR_SPACE = -4
+
+CEV_F32 = 0
+CEV_BF16 = 1
+CEV_MAX_SPANS = 4
+
+i32 = C.c_int32
+i64 = C.c_int64
+
+
+class Span(C.Structure):
+    _fields_ = [("begin", i32), ("len", i32)]
+
+
+class Block(C.Structure):
+    _fields_ = [
+        ("q_begin", i32),
+        ("q_len", i32),
+        ("valid_len", i32),
+        ("causal", i32),
+        ("local_begin", i32),
+        ("n_spans", i32),
+        ("spans", Span * CEV_MAX_SPANS),
+    ]
+
+    def as_tuple(self):
+        return (self.q_begin, self.q_len, self.valid_len, self.causal, self.local_begin,
+                tuple((self.spans[i].begin, self.spans[i].len) for i in range(self.n_spans)))
+
+
+class AttnDesc(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("n_q_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
+        ("t", i32), ("s_cache", i32), ("scale", C.c_float), ("has_gate", i32),
+        ("q_stride_t", i64), ("q_stride_h", i64),
+        ("kc_stride_s", i64), ("kc_stride_h", i64),
+        ("vc_stride_s", i64), ("vc_stride_h", i64),
+        ("kn_stride_t", i64), ("kn_stride_h", i64),
+        ("vn_stride_t", i64), ("vn_stride_h", i64),
+        ("g_stride_t", i64), ("g_stride_h", i64),
+        ("o_stride_t", i64), ("o_stride_h", i64),
+    ]
+
+
+class QkNormDesc(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("n_q_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
+        ("t", i32), ("rotary_dim", i32), ("n_pos", i32), ("weight_plus_one", i32),
+        ("eps", C.c_float),
+        ("qi_stride_t", i64), ("qi_stride_h", i64),
+        ("ki_stride_t", i64), ("ki_stride_h", i64),
+        ("qo_stride_t", i64), ("qo_stride_h", i64),
+        ("ko_stride_t", i64), ("ko_stride_h", i64),
+    ]
+
+
+P = C.c_void_p
+Pi32 = C.POINTER(i32)
+PBlock = C.POINTER(Block)
+
+# name -> (restype, argtypes); the exact list of symbols include/cev_hip.h declares.
+SIGNATURES = {
+    "cev_attn_desc_init": (i32, [C.POINTER(AttnDesc), i32, i32, i32, i32, i32, i32, i32]),
+    "cev_attn_plan_size": (i32, [C.POINTER(AttnDesc), PBlock, i32, C.POINTER(C.c_size_t)]),
+    "cev_attn_plan_build": (i32, [C.POINTER(AttnDesc), PBlock, i32, P, C.c_size_t]),
+    "cev_packed_attention": (i32, [C.POINTER(AttnDesc), P, P, P, P, P, P, P, P, P, P]),
+    "cev_qknorm_desc_init": (i32, [C.POINTER(QkNormDesc), i32, i32, i32, i32, i32, i32, i32, i32, C.c_float, i32]),
+    "cev_qknorm_rope": (i32, [C.POINTER(QkNormDesc), P, P, P, P, P, P, P, P, P, P]),
+    "cev_rope_table": (i32, [C.c_double, i32, i32, i32, P, P]),
+    "cev_table_from_plans": (i32, [i32, Pi32, Pi32, Pi32, i32, Pi32, Pi32, PBlock, i32, Pi32, Pi32, i32, Pi32, Pi32]),
+    "cev_table_from_rows": (i32, [i32, i32, i32, i32, Pi32, PBlock, i32]),
+    "cev_table_from_segment_ids": (i32, [C.POINTER(C.c_uint32), i32, i32, PBlock, i32, Pi32]),
+    "cev_table_to_dense_mask": (i32, [PBlock, i32, i32, i32, P]),
+    "cev_table_from_dense_mask": (i32, [P, i32, i32, PBlock, i32, Pi32]),
+    "cev_last_error": (C.c_char_p, []),
+    "cev_abi_version": (i32, []),
+    "cev_device_info": (i32, [i32, C.c_char_p, C.c_size_t, Pi32, C.POINTER(i64), Pi32]),
+    "cev_malloc": (i32, [C.POINTER(P), C.c_size_t]),
+    "cev_free": (i32, [P]),
+    "cev_memcpy_h2d": (i32, [P, P, C.c_size_t, P]),
+    "cev_memcpy_d2h": (i32, [P, P, C.c_size_t, P]),
+    "cev_stream_create": (i32, [C.POINTER(P)]),
+    "cev_stream_destroy": (i32, [P]),
+    "cev_stream_synchronize": (i32, [P]),
+}
+
+_lib = None
+
+
+class CevError(RuntimeError):
+    """A failed C-ABI call: `code` is the CEV_ERR_* status."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"cev error {code}: {msg}")
+        self.code = code
+
+
+def lib():
+    """The loaded libcev_hip.so.  There is no fallback: without the built
+    library every entry point raises."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != CEV_OK:
+        raise CevError(rc, lib().cev_last_error().decode(errors="replace"))

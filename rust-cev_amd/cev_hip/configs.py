@@ -1,0 +1,152 @@
+"""The synthetic workloads of this path as concrete shapes and seeded inputs.
+
+Every tensor comes from cev_hip.synth with seed = workload number and its own
+stream id, so the GPU run and the CPU checker see identical values.  Arrays
+are f32 (holding bf16-exact values for bf16 workloads).
+
+  c1  Qwen3-0.6B-shaped attention layer, f32: cached prefix P=256 (Hkv=8,
+      d=128, post-RoPE K/V), 4 questions x 3 rotations = 12 blocks x 32 tokens,
+      Hq=16, positions restart at 256 per block (engine.rs:411).
+  c3  Qwen3-8B-shaped layer, bf16: P=32768, 64 blocks x 64 tokens, Hq=32,
+      Hkv=8, d=128, positions restart at 32768.
+  c4  Qwen3.5-style gated layer, bf16, bidirectional (d3): one 8192-token row,
+      Hq=16, Hkv=4, d=256, rotary 64 of 256 dims (theta 1e7), weight 1 + w,
+      sigmoid output gate.
+  c5a the gated-attention half of the hybrid pair: 32 rows right-padded to
+      64 tokens continue a 4096-token prefix (Hq=16, Hkv=4, d=256).
+  hbm the long-prefix short-suffix shape: c3 with 1 block x 16 tokens.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional, Tuple
+
+import numpy as np
+
+from . import synth
+
+# stream ids
+S_PK, S_PV, S_Q, S_K, S_V, S_WQ, S_WK, S_GATE, S_LEN, S_WO, S_WR = range(1, 12)
+
+
+@dataclass
+class AttnWorkload:
+    name: str
+    seed: int
+    bf16: bool
+    hq: int
+    hkv: int
+    d: int
+    prefix: int                     # cached keys (post-RoPE prefix K/V)
+    blocks: List[int]               # suffix block lengths (packed in order)
+    theta: float
+    rotary_dim: int
+    causal: bool = True
+    gated: bool = False
+    plus_one: bool = False          # Qwen3.5 RMSNorm weight 1 + w
+    eps: float = 1e-6
+    lengths: Optional[List[int]] = None   # real tokens per row (padded rows)
+    pos0: Optional[int] = None      # first suffix position (default: prefix)
+    notes: str = ""
+
+    @property
+    def t(self) -> int:
+        return int(sum(self.blocks))
+
+    @property
+    def g(self) -> int:
+        return self.hq // self.hkv
+
+    def positions(self) -> np.ndarray:
+        p0 = self.prefix if self.pos0 is None else self.pos0
+        return np.concatenate([p0 + np.arange(L, dtype=np.int32) for L in self.blocks]).astype(np.int32)
+
+    def n_pos(self) -> int:
+        return int(self.positions().max()) + 1
+
+    def block_starts(self) -> np.ndarray:
+        return np.concatenate([[0], np.cumsum(self.blocks)[:-1]]).astype(np.int64)
+
+    def useful_pairs(self) -> int:
+        """Unmasked (query row, key) pairs per query head."""
+        tot = 0
+        for i, L in enumerate(self.blocks):
+            if self.causal:
+                tot += L * self.prefix + L * (L + 1) // 2
+            else:
+                v = L if self.lengths is None else self.lengths[i]
+                tot += L * self.prefix + v * L + (L - v)
+        return tot
+
+    def useful_flops(self) -> float:
+        """Unmasked pairs x 4d (QK^T and PV) over all query heads."""
+        return 4.0 * self.d * self.hq * self.useful_pairs()
+
+    def alg_bytes(self) -> int:
+        """Q, K/V (prefix + new), O and the gate, each once, in the config dtype."""
+        e = 2 if self.bf16 else 4
+        t = self.t
+        n = t * self.hq * self.d * 2 + 2 * (self.prefix + t) * self.hkv * self.d
+        if self.gated:
+            n += t * self.hq * self.d
+        return n * e
+
+    # ---- inputs -------------------------------------------------------
+    def prefix_kv(self, kv_heads: Optional[Tuple[int, int]] = None):
+        """(hkv, P, d) post-RoPE cached K and V."""
+        shape = (self.hkv, self.prefix, self.d)
+        return (synth.tensor(self.seed, S_PK, shape, self.bf16), synth.tensor(self.seed, S_PV, shape, self.bf16))
+
+    def suffix_qkv(self):
+        """Pre-norm q (t, hq, d) [or the gated (t, hq, 2d) q_proj output], k and v (t, hkv, d)."""
+        t = self.t
+        qd = 2 * self.d if self.gated else self.d
+        q = synth.tensor(self.seed, S_Q, (t, self.hq, qd), self.bf16)
+        k = synth.tensor(self.seed, S_K, (t, self.hkv, self.d), self.bf16)
+        v = synth.tensor(self.seed, S_V, (t, self.hkv, self.d), self.bf16)
+        return q, k, v
+
+    def norm_weights(self):
+        """QK-norm weights: 1 + 0.1 N(0,1) as stored (Qwen3), or 0.1 N(0,1)
+        as stored for the zero-centred form (Qwen3.5 applies 1 + w)."""
+        off = 0.0 if self.plus_one else 1.0
+        wq = synth.tensor(self.seed, S_WQ, (self.d,), self.bf16, scale=0.1, offset=off)
+        wk = synth.tensor(self.seed, S_WK, (self.d,), self.bf16, scale=0.1, offset=off)
+        return wq, wk
+
+    def plans_items(self):
+        """engine.rs packing: one plan whose whole prefix is cached, one
+        question item per block."""
+        return [(self.prefix, self.prefix, self.prefix)], [(0, L) for L in self.blocks]
+
+
+def c1() -> AttnWorkload:
+    return AttnWorkload("c1", 1, False, 16, 8, 128, 256, [32] * 12, 1e6, 128,
+                        notes="Qwen3-0.6B-shaped layer, f32, 12 x 32 blocks after P=256")
+
+
+def c3(blocks: int = 64, block_len: int = 64) -> AttnWorkload:
+    return AttnWorkload("c3", 3, True, 32, 8, 128, 32768, [block_len] * blocks, 1e6, 128,
+                        notes="Qwen3-8B-shaped layer, bf16, 64 x 64 blocks after P=32768")
+
+
+def hbm(blocks: int = 1) -> AttnWorkload:
+    w = c3(blocks, 16)
+    w.name = f"hbm{blocks}x16"
+    w.notes = f"c3 prefix with {blocks} x 16 suffix tokens (KV-streaming bound)"
+    return w
+
+
+def c4() -> AttnWorkload:
+    return AttnWorkload("c4", 4, True, 16, 4, 256, 0, [8192], 1e7, 64, causal=False, gated=True, plus_one=True,
+                        lengths=[8192], pos0=0, notes="Qwen3.5-style gated layer, bf16, bidirectional 8192-token row")
+
+
+def c5_attention() -> AttnWorkload:
+    n_rows, t = 32, 64
+    lengths = (33 + np.floor(synth.uniform(5, S_LEN, n_rows) * 32)).astype(int).tolist()
+    return AttnWorkload("c5a", 5, True, 16, 4, 256, 4096, [t] * n_rows, 1e7, 64, causal=True, gated=True, plus_one=True,
+                        lengths=lengths, notes="Qwen3.5 gated attention: 32 rows padded to 64 after P=4096")
+
+
+WORKLOADS = {"c1": c1, "c3": c3, "c4": c4, "c5a": c5_attention, "hbm": hbm}

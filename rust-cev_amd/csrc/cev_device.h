@@ -1,0 +1,28 @@
+// Device-side helpers for the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Round-to-nearest-even f32 -> bf16 -> f32 (the value the model dtype holds).
+__device__ __forceinline__ float bf16_round(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float((u | 0x00400000u) & 0xffff0000u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) {
+  return (uint16_t)(__float_as_uint(bf16_round(x)) >> 16);
+}
+
+__device__ __forceinline__ float bf16_from_bits(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Exchange a value with the lane 32 away (the other half of a wave64).
+__device__ __forceinline__ float swap_half(float x) { return __shfl_xor(x, 32, 64); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -1,0 +1,16 @@
+// Internal helpers shared by the host code and the launchers.
+#pragma once
+#include <stdarg.h>
+#include <stdint.h>
+
+#include "../../include/cev_hip.h"
+
+// Records a formatted thread-local message for cev_last_error() and returns
+// `code`, so call sites read `return cev_fail(CEV_ERR_INVALID, "...", ...)`.
+int32_t cev_fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void cev_clear_error();
+
+#define CEV_CHECK_ARG(cond, ...)                      \
+  do {                                                \
+    if (!(cond)) return cev_fail(CEV_ERR_INVALID, __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,233 @@
+"""CPU tests of libcev_hip.so: it loads, exports every symbol the header
+declares, validates inputs before any launch, and its host table builders
+reproduce the reference's dense masks exactly (the masks come from the
+oracle's restatement of engine.rs:418-442, qwen3.rs:157-169,
+qwen35.rs:471-498)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import cev_hip
+from cev_hip import _abi
+from cev_hip._abi import CEV_BF16, CEV_ERR_INVALID, CEV_ERR_SPACE, CEV_ERR_UNSUPPORTED, CEV_F32, CevError
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+RNG = np.random.default_rng(7)
+
+
+def _header_symbols():
+    src = open(os.path.join(ROOT, "include", "cev_hip.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(cev_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_header_symbol(cev):
+    syms = _header_symbols()
+    assert len(syms) >= 20
+    L = _abi.lib()
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    assert set(syms) == set(_abi.SIGNATURES), "ctypes signatures and header disagree"
+    assert L.cev_abi_version() == 1
+
+
+def test_desc_init_layouts(cev):
+    d = cev_hip.attn_desc(CEV_BF16, 32, 8, 128, 4096, 32768)
+    assert d.q_stride_t == 32 * 128 and d.q_stride_h == 128
+    assert d.kc_stride_h == 32768 * 128 and d.kc_stride_s == 128
+    assert d.kn_stride_t == 8 * 128 and d.kn_stride_h == 128
+    assert np.float32(d.scale) == np.float32(1 / np.sqrt(128))  # f32, as qwen3.rs:207 + affine
+
+
+def _plan_rc(desc, blocks):
+    arr = (_abi.Block * max(1, len(blocks)))(*blocks)
+    size = C.c_size_t()
+    return _abi.lib().cev_attn_plan_size(C.byref(desc), arr, len(blocks), C.byref(size))
+
+
+B = cev_hip.BlockTable.block
+
+
+@pytest.mark.parametrize("blocks,code", [
+    ([B(0, 0, 10)], CEV_ERR_INVALID),                                  # q_len 0
+    ([B(0, 4, 10), B(2, 4, 14)], CEV_ERR_INVALID),                      # overlapping rows
+    ([B(0, 4, 10, spans=[(0, 11)])], CEV_ERR_INVALID),                  # span overlaps own keys
+    ([B(0, 4, 10, spans=[(0, 5), (4, 3)])], CEV_ERR_INVALID),           # overlapping spans
+    ([B(0, 4, 10, spans=[(20, 5)])], CEV_ERR_INVALID),                  # span past S
+    ([B(6, 4, 10)], CEV_ERR_INVALID),                                   # rows past t
+    ([B(0, 4, 10, causal=False, valid_len=5)], CEV_ERR_INVALID),        # valid_len > q_len
+    ([B(0, 4, 10, causal=True, valid_len=3)], CEV_ERR_INVALID),         # causal with padding
+])
+def test_malformed_tables_are_rejected(cev, blocks, code):
+    d = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 8, 10)
+    assert _plan_rc(d, blocks) == code
+    assert _abi.lib().cev_last_error()
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(head_dim=64), CEV_ERR_UNSUPPORTED),
+    (dict(n_q_heads=12, n_kv_heads=4), CEV_ERR_UNSUPPORTED),   # g = 3
+    (dict(n_q_heads=10, n_kv_heads=4), CEV_ERR_INVALID),       # not a multiple
+    (dict(dtype=7), CEV_ERR_UNSUPPORTED),
+    (dict(q_stride_h=100), CEV_ERR_UNSUPPORTED),               # misaligned rows
+    (dict(t=-1), CEV_ERR_INVALID),
+])
+def test_unsupported_descriptors_are_rejected(cev, kw, code):
+    d = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 8, 10)
+    for k, v in kw.items():
+        setattr(d, k, v)
+    assert _plan_rc(d, [B(0, 8, 10, spans=[(0, 10)])]) == code
+
+
+def test_f32_head_dim_256_is_unsupported(cev):
+    d = cev_hip.attn_desc(CEV_F32, 8, 2, 256, 8, 10)
+    assert _plan_rc(d, [B(0, 8, 10, spans=[(0, 10)])]) == CEV_ERR_UNSUPPORTED
+
+
+def test_plan_buffer_too_small(cev):
+    d = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 8, 10)
+    arr = (_abi.Block * 1)(B(0, 8, 10, spans=[(0, 10)]))
+    buf = np.zeros(64, np.uint8)
+    off = (-buf.ctypes.data) % 16
+    rc = _abi.lib().cev_attn_plan_build(C.byref(d), arr, 1, C.c_void_p(buf.ctypes.data + off), 32)
+    assert rc == CEV_ERR_SPACE
+
+
+def test_launch_validates_before_any_gpu_call(cev):
+    d = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 8, 10)
+    tab = cev_hip.BlockTable([B(0, 8, 10, spans=[(0, 10)])], 8, 10)
+    plan = cev_hip.AttnPlan(d, tab)
+    L = _abi.lib()
+    fake = C.c_void_p(4096)
+    # null plan / null buffers / a plan for other shapes: all fail before a launch
+    assert L.cev_packed_attention(C.byref(d), None, None, fake, fake, fake, fake, fake, None, fake, None) == CEV_ERR_INVALID
+    hp = C.c_void_p(plan.host.ctypes.data)
+    assert L.cev_packed_attention(C.byref(d), hp, fake, None, fake, fake, fake, fake, None, fake, None) == CEV_ERR_INVALID
+    d2 = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 9, 10)
+    assert L.cev_packed_attention(C.byref(d2), hp, fake, fake, fake, fake, fake, fake, None, fake, None) == CEV_ERR_INVALID
+    assert L.cev_packed_attention(C.byref(d), hp, fake, fake, None, None, fake, fake, None, fake, None) == CEV_ERR_INVALID
+    d.has_gate = 1
+    assert L.cev_packed_attention(C.byref(d), hp, fake, fake, fake, fake, fake, fake, None, fake, None) == CEV_ERR_INVALID
+
+
+def test_empty_table_needs_no_launch(cev):
+    d = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 8, 10)
+    plan = cev_hip.AttnPlan(d, cev_hip.BlockTable([], 8, 10))
+    assert plan.n_tiles == 0
+    hp = C.c_void_p(plan.host.ctypes.data)
+    assert _abi.lib().cev_packed_attention(C.byref(d), hp, hp, None, None, None, None, None, None, None, None) == 0
+
+
+def test_qknorm_validation(cev):
+    L = _abi.lib()
+    d = _abi.QkNormDesc()
+    assert L.cev_qknorm_desc_init(C.byref(d), CEV_BF16, 8, 2, 128, 4, 130, 10, 0, 1e-6, 0) == 0
+    assert L.cev_qknorm_rope(C.byref(d), None, None, None, None, None, None, None, None, None, None) == CEV_ERR_INVALID
+    d.rotary_dim = 128
+    d.head_dim = 96
+    assert L.cev_qknorm_rope(C.byref(d), None, None, None, None, None, None, None, None, None, None) == CEV_ERR_UNSUPPORTED
+
+
+# ---------------------------------------------------------------- table builders vs reference masks
+
+
+def _random_pass(rng):
+    n_plans = int(rng.integers(1, 4))
+    plans = []
+    for _ in range(n_plans):
+        prefix = int(rng.integers(1, 40))
+        mode = rng.integers(0, 3)
+        if mode == 0:       # cached prefix, no tail
+            plans.append((prefix, prefix, prefix))
+        elif mode == 1:     # head prefilled, tail in the pass
+            tail = int(rng.integers(1, prefix + 1))
+            plans.append((prefix - tail, prefix, prefix - tail))
+        else:               # nothing cached, whole prefix is the tail
+            plans.append((0, prefix, 0))
+    items = [(int(rng.integers(0, n_plans)), int(rng.integers(1, 12))) for _ in range(int(rng.integers(1, 7)))]
+    return plans, items
+
+
+def test_table_from_plans_reproduces_engine_mask(cev, orc):
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        plans, items = _random_pass(rng)
+        ep = orc.engine_pass(plans, items)
+        tab, pos, gather = cev_hip.BlockTable.from_plans(plans, items)
+        assert tab.t == ep["n"] and tab.s_cache == ep["past_total"]
+        assert np.array_equal(tab.to_dense_mask(), ep["mask"])
+        assert np.array_equal(pos, ep["pos"]) and np.array_equal(gather, ep["gather"])
+        back = cev_hip.BlockTable.from_dense_mask(ep["mask"], ep["past_total"])
+        assert np.array_equal(back.to_dense_mask(), ep["mask"])
+
+
+def test_table_from_segments_reproduces_segment_mask(cev, orc):
+    for past, seg in ((0, [0] * 9), (12, [0] * 5), (7, [0, 0, 1, 1, 1, 2, 3, 3])):
+        tab = cev_hip.BlockTable.from_segment_ids(seg, past)
+        assert np.array_equal(tab.to_dense_mask(), orc.segment_mask(seg, past))
+    with pytest.raises(CevError):
+        cev_hip.BlockTable.from_segment_ids([0, 1, 0], 3)
+
+
+def test_table_from_rows_reproduces_qwen35_masks(cev, orc):
+    b, t, past = 3, 6, 10
+    tab = cev_hip.BlockTable.from_rows(b, t, past, causal=True)
+    # rows of a batch each see the (broadcast) prefix and their own row causally
+    dense = tab.to_dense_mask()
+    br = orc.branch_mask(t, past)
+    for r in range(b):
+        rows = dense[r * t:(r + 1) * t]
+        assert np.array_equal(rows[:, :past], br[:, :past])
+        assert np.array_equal(rows[:, past + r * t: past + (r + 1) * t], br[:, past:])
+        others = np.delete(rows[:, past:], np.s_[r * t:(r + 1) * t], axis=1)
+        assert np.all(np.isneginf(others))
+    lengths = [6, 2, 0]
+    tab = cev_hip.BlockTable.from_rows(b, t, 0, causal=False, lengths=lengths)
+    dense = tab.to_dense_mask()
+    bd = orc.bidirectional_mask(t, lengths)
+    for r in range(b):
+        assert np.array_equal(dense[r * t:(r + 1) * t, r * t:(r + 1) * t], bd[r])
+    back = cev_hip.BlockTable.from_dense_mask(dense, 0)
+    assert np.array_equal(back.to_dense_mask(), dense)
+    with pytest.raises(CevError):
+        cev_hip.BlockTable.from_rows(2, 4, 5, causal=False, lengths=[4, 4])
+
+
+def test_rope_table_is_the_reference_recipe(cev, orc):
+    for theta, rot, n in ((1e6, 128, 3000), (1e7, 64, 9000)):
+        c, s = cev_hip.rope_table(theta, rot, n, CEV_F32)
+        oc, os_ = orc.rope_table(theta, rot, n, False)
+        assert np.array_equal(c, oc) and np.array_equal(s, os_)
+        cb, sb = cev_hip.rope_table(theta, rot, n, CEV_BF16)
+        ocb, osb = orc.rope_table(theta, rot, n, True)
+        assert np.array_equal((cb.astype(np.uint32) << 16).view(np.float32), ocb)
+        assert np.array_equal((sb.astype(np.uint32) << 16).view(np.float32), osb)
+
+
+def test_plan_tiles_cover_rows_and_keys(cev, orc):
+    """The compiled plan visits exactly the keys each row may see."""
+    rng = np.random.default_rng(11)
+    for _ in range(60):
+        plans, items = _random_pass(rng)
+        tab, _, _ = cev_hip.BlockTable.from_plans(plans, items)
+        for hq, hkv in ((8, 8), (8, 4), (8, 2), (8, 1)):
+            d = cev_hip.attn_desc(CEV_BF16, hq, hkv, 128, tab.t, tab.s_cache)
+            plan = cev_hip.AttnPlan(d, tab)
+            dense = tab.to_dense_mask() == 0
+            rows = plan.host.view(np.int32)[plan.host[:64].view(np.int32)[13]:].reshape(-1, 4)[: tab.t]
+            seen = np.zeros_like(dense)
+            for tr0, tn, s0, sn in plan.tiles():
+                assert tn <= plan.tile_rows
+                for kb, ke, masked, _ in plan.segs()[s0:s0 + sn]:
+                    assert (kb < tab.s_cache) == (ke <= tab.s_cache) or kb >= tab.s_cache
+                    for r in range(tr0, tr0 + tn):
+                        keys = np.arange(kb, ke)
+                        if masked:
+                            lo, hi, dg, _ = rows[r]
+                            keys = keys[((keys >= lo) & (keys < hi)) | (keys == dg)]
+                        assert not seen[r, keys].any(), "a key visited twice"
+                        seen[r, keys] = True
+            assert np.array_equal(seen, dense)

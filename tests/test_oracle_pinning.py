@@ -1,0 +1,400 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+Each oracle function is checked against something outside itself: the
+reference's own unit-test vectors (qwen35.rs:758-822), closed forms, textbook
+special cases, a second independent implementation (f64 brute force, torch),
+or hand-derived known answers from reading the reference.  Every `*_catches`
+test plants a plausible mistake in the oracle (cev_oracle.c MUT_*) and shows
+that the same check then fails.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from cev_hip import synth
+
+RNG = np.random.default_rng(12345)
+
+
+# ---------------------------------------------------------------- bf16 rounding
+
+
+def test_bf16_rounding_known_answers(orc):
+    x = np.array([1.0, 1 + 2**-8, 1 + 3 * 2**-8, -2.5, 3.0e38, 1e-40, 0.0], np.float32)
+    want = np.array([1.0, 1.0, 1 + 2**-6, -2.5], np.float32)
+    got = orc.round_bf16(x)
+    assert np.array_equal(got[:4], want)  # ties to even
+    assert math.isinf(float(orc.round_bf16(np.array([3.4e38], np.float32))[0]))
+
+
+def test_bf16_rounding_matches_torch(orc):
+    x = (RNG.standard_normal(100000) * 10.0 ** RNG.integers(-6, 6, 100000)).astype(np.float32)
+    t = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(orc.round_bf16(x), t)
+    assert np.array_equal(synth.round_bf16(x), t)
+
+
+# ---------------------------------------------------------------- RoPE table
+
+
+def _table_closed_form(theta, rot, n_pos):
+    half = rot // 2
+    inv = np.array([np.float32(1.0) / np.float32(theta ** (2 * i / rot)) for i in range(half)], np.float32)
+    ang = (np.arange(n_pos, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    return np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))
+
+
+def _check_table(orc, theta=1e6, rot=128, n_pos=4096):
+    c, s = orc.rope_table(theta, rot, n_pos, False)
+    cw, sw = _table_closed_form(theta, rot, n_pos)
+    ulp = np.spacing(np.float32(1.0))
+    return (np.abs(c - cw).max() <= ulp and np.abs(s - sw).max() <= ulp and np.all(c[0] == 1.0) and np.all(s[0] == 0.0))
+
+
+def test_rope_table_closed_form(orc):
+    assert _check_table(orc)
+    assert _check_table(orc, theta=1e7, rot=64, n_pos=8200)
+
+
+def test_rope_table_catches_shifted_position(orc):
+    with oracle.mutation(oracle.MUT_TABLE_POS):
+        assert not _check_table(orc)
+
+
+def test_rope_table_bf16_is_rounded_f32(orc):
+    c, s = orc.rope_table(1e6, 128, 600, False)
+    cb, sb = orc.rope_table(1e6, 128, 600, True)
+    assert np.array_equal(cb, orc.round_bf16(c)) and np.array_equal(sb, orc.round_bf16(s))
+
+
+# ---------------------------------------------------------------- RMSNorm
+
+
+def _check_norm(orc):
+    # closed form: d=2, x=(3,4), w=1 -> x / sqrt(12.5 + eps)
+    y = orc.rms_norm(np.array([[3.0, 4.0]], np.float32), np.ones(2, np.float32), 1e-6, False)
+    want = np.array([3.0, 4.0]) / math.sqrt(12.5 + 1e-6)
+    ok = np.abs(y[0] - want).max() < 1e-6
+    # unit RMS with w = 1
+    x = RNG.standard_normal((64, 128)).astype(np.float32)
+    y = orc.rms_norm(x, np.ones(128, np.float32), 1e-6, False)
+    ok &= np.abs((y.astype(np.float64) ** 2).mean(-1) - 1.0).max() < 5e-6
+    return bool(ok)
+
+
+def test_rms_norm_closed_forms(orc):
+    assert _check_norm(orc)
+
+
+def test_rms_norm_catches_wrong_mean(orc):
+    with oracle.mutation(oracle.MUT_NORM_DIM_M1):
+        assert not _check_norm(orc)
+
+
+def test_rms_norm_scale_invariance_and_weights(orc):
+    x = RNG.standard_normal((32, 256)).astype(np.float32)
+    w = (1 + 0.1 * RNG.standard_normal(256)).astype(np.float32)
+    a = orc.rms_norm(x, w, 0.0, False)
+    b = orc.rms_norm(x * np.float32(8.0), w, 0.0, False)  # eps 0 and a power of two: exact
+    assert np.array_equal(a, b)
+    # zero-centred weights (qwen35.rs:169): (1 + w) rounded to the dtype
+    for bf in (False, True):
+        xb = orc.round_bf16(x) if bf else x
+        wz = orc.round_bf16(0.1 * w) if bf else (0.1 * w).astype(np.float32)
+        one_plus = orc.round_bf16(wz + 1) if bf else (wz + 1).astype(np.float32)
+        assert np.array_equal(orc.rms_norm(xb, wz, 1e-6, bf, plus_one=True), orc.rms_norm(xb, one_plus, 1e-6, bf))
+
+
+# ---------------------------------------------------------------- RoPE
+
+
+def _check_rope_basis(orc, rot=128, d=128):
+    c, s = orc.rope_table(1e6, rot, 300, False)
+    half = rot // 2
+    ok = True
+    for i in (0, 5, half - 1):
+        for p in (0, 7, 299):
+            x = np.zeros((1, 2, d), np.float32)
+            x[0, 0, i] = 1.0          # e_i      -> (c, s) at (i, i + half)
+            x[0, 1, i + half] = 1.0   # e_{i+h}  -> (-s, c)
+            y = orc.rope(x, np.array([p], np.int32), c, s, rot, False)
+            ok &= y[0, 0, i] == c[p, i] and y[0, 0, i + half] == s[p, i]
+            ok &= y[0, 1, i] == -s[p, i] and y[0, 1, i + half] == c[p, i]
+            ok &= np.count_nonzero(y[0, :, rot:]) == 0
+    return bool(ok)
+
+
+def test_rope_basis_vectors(orc):
+    assert _check_rope_basis(orc)
+    assert _check_rope_basis(orc, rot=64, d=256)
+
+
+def test_rope_catches_sign(orc):
+    with oracle.mutation(oracle.MUT_ROPE_SIN_SIGN):
+        assert not _check_rope_basis(orc)
+
+
+def test_rope_preserves_norm_and_relative_position(orc):
+    c, s = orc.rope_table(1e6, 128, 512, False)
+    x = RNG.standard_normal((6, 4, 128)).astype(np.float32)
+    pos = np.array([0, 3, 100, 200, 300, 511], np.int32)
+    y = orc.rope(x, pos, c, s, 128, False)
+    assert np.allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=2e-6)
+    q = RNG.standard_normal((1, 1, 128)).astype(np.float32)
+    k = RNG.standard_normal((1, 1, 128)).astype(np.float32)
+    dots = []
+    for shift in (0, 17, 150):  # <R(p)q, R(p')k> depends only on p - p'
+        rq = orc.rope(q, np.array([40 + shift], np.int32), c, s, 128, False)
+        rk = orc.rope(k, np.array([10 + shift], np.int32), c, s, 128, False)
+        dots.append(float((rq.astype(np.float64) * rk).sum()))
+    assert max(dots) - min(dots) < 1e-4 * (1 + abs(dots[0]))
+
+
+# ---------------------------------------------------------------- attention
+
+
+def _two_key_case():
+    d = 8
+    q = np.zeros((1, 1, d), np.float32)
+    q[0, 0, :2] = [1.7, -0.4]
+    k = np.zeros((1, 2, d), np.float32)
+    k[0, 0, 0] = 1.0
+    k[0, 1, 1] = 1.0
+    v = np.zeros((1, 2, d), np.float32)
+    v[0, 0, 0] = 1.0
+    v[0, 1, 1] = 1.0
+    mask = np.zeros((1, 2), np.float32)
+    p1 = 1.0 / (1.0 + math.exp((-0.4 - 1.7) / math.sqrt(d)))
+    return q, k, v, mask, p1
+
+
+def _check_two_key(orc):
+    q, k, v, mask, p1 = _two_key_case()
+    o = orc.attend(q, k, v, mask, False)[0, 0, 0]
+    return abs(o[0] - p1) < 1e-6 and abs(o[1] - (1 - p1)) < 1e-6 and np.count_nonzero(o[2:]) == 0
+
+
+def test_attend_two_key_closed_form(orc):
+    assert _check_two_key(orc)
+
+
+@pytest.mark.parametrize("mut", [oracle.MUT_ATTN_NO_SCALE, oracle.MUT_ATTN_V_SHIFT])
+def test_attend_two_key_catches(orc, mut):
+    with oracle.mutation(mut):
+        assert not _check_two_key(orc)
+
+
+def _mask_case(orc):
+    plans = [(40, 40, 40), (24, 30, 24)]
+    items = [(0, 5), (1, 1), (0, 7), (1, 3)]
+    return orc.engine_pass(plans, items)
+
+
+def _check_identical_keys(orc):
+    ep = _mask_case(orc)
+    n, s = ep["n"], ep["past_total"] + ep["n"]
+    mask = ep["mask"]
+    q = RNG.standard_normal((2, n, 16)).astype(np.float32)
+    k = np.broadcast_to(RNG.standard_normal(16).astype(np.float32), (1, s, 16)).copy()
+    v = RNG.standard_normal((1, s, 16)).astype(np.float32)
+    o = orc.attend(q, k, v, mask, False)[0]
+    vis = (mask == 0).astype(np.float64)
+    want = (vis @ v[0].astype(np.float64)) / vis.sum(1, keepdims=True)
+    return bool(np.abs(o - want[None]).max() < 2e-6)
+
+
+def test_attend_identical_keys_give_mean_of_visible_values(orc):
+    assert _check_identical_keys(orc)
+
+
+def test_attend_identical_keys_catches_value_shift(orc):
+    with oracle.mutation(oracle.MUT_ATTN_V_SHIFT):
+        assert not _check_identical_keys(orc)
+
+
+def test_attend_zero_query_uniform_and_constant_values(orc):
+    ep = _mask_case(orc)
+    n, s = ep["n"], ep["past_total"] + ep["n"]
+    mask = ep["mask"]
+    k = RNG.standard_normal((1, s, 32)).astype(np.float32)
+    v = RNG.standard_normal((1, s, 32)).astype(np.float32)
+    o = orc.attend(np.zeros((1, n, 32), np.float32), k, v, mask, False)[0, 0]
+    vis = (mask == 0).astype(np.float64)
+    assert np.abs(o - (vis @ v[0]) / vis.sum(1, keepdims=True)).max() < 2e-6
+    q = RNG.standard_normal((1, n, 32)).astype(np.float32)
+    vc = np.broadcast_to(np.linspace(-2, 2, 32, dtype=np.float32), (1, s, 32)).copy()
+    o = orc.attend(q, k, vc, mask, False)[0, 0]
+    assert np.abs(o - vc[0, 0]).max() < 2e-6
+
+
+def _check_gqa(orc):
+    t, s, d = 6, 11, 16
+    q = RNG.standard_normal((8, t, d)).astype(np.float32)
+    k = RNG.standard_normal((2, s, d)).astype(np.float32)
+    v = RNG.standard_normal((2, s, d)).astype(np.float32)
+    mask = orc.branch_mask(t, s - t)
+    a = orc.attend(q, k, v, mask, False)
+    b = orc.attend(q, np.repeat(k, 4, axis=0), np.repeat(v, 4, axis=0), mask, False)
+    return bool(np.array_equal(a, b))
+
+
+def test_attend_gqa_equals_mha_with_repeated_heads(orc):
+    assert _check_gqa(orc)
+
+
+def test_attend_gqa_catches_head_map(orc):
+    with oracle.mutation(oracle.MUT_ATTN_KV_MODULO):
+        assert not _check_gqa(orc)
+
+
+def test_attend_f32_matches_f64_textbook(orc):
+    ep = _mask_case(orc)
+    n, s = ep["n"], ep["past_total"] + ep["n"]
+    q = RNG.standard_normal((4, n, 128)).astype(np.float32)
+    k = RNG.standard_normal((2, s, 128)).astype(np.float32)
+    v = RNG.standard_normal((2, s, 128)).astype(np.float32)
+    a = orc.attend(q, k, v, ep["mask"], False)
+    b = orc.attend_f64(q, k, v, ep["mask"])
+    assert np.abs(a - b).max() < 2e-6
+    ab = orc.attend(orc.round_bf16(q), orc.round_bf16(k), orc.round_bf16(v), ep["mask"], True)
+    bb = orc.attend_f64(orc.round_bf16(q), orc.round_bf16(k), orc.round_bf16(v), ep["mask"])
+    assert np.abs(ab - bb).max() < 2e-2
+
+
+def test_attend_bidirectional_key_permutation(orc):
+    t, d = 9, 32
+    lengths = [9, 6]
+    mask = orc.bidirectional_mask(t, lengths)
+    q = RNG.standard_normal((2, 2, t, d)).astype(np.float32)
+    k = RNG.standard_normal((2, 1, t, d)).astype(np.float32)
+    v = RNG.standard_normal((2, 1, t, d)).astype(np.float32)
+    a = orc.attend(q, k, v, mask, False)
+    perm = np.array([3, 1, 4, 0, 5, 2, 6, 7, 8])  # permutes real keys of both rows
+    b = orc.attend(q, k[:, :, perm], v[:, :, perm], mask[:, :, perm], False)
+    assert np.abs(a - b).max() < 2e-6
+
+
+# ---------------------------------------------------------------- masks
+
+
+def test_engine_mask_known_answer(orc):
+    # past 2, prefix 3 with a 1-token tail, one 2-token question (engine.rs:389-442)
+    ep = orc.engine_pass([(2, 3, 2)], [(0, 2)])
+    z, n_ = 0.0, -np.inf
+    want = np.array([[z, z, z, n_, n_], [z, z, z, z, n_], [z, z, z, z, z]], np.float32)
+    assert np.array_equal(ep["mask"], want)
+    assert ep["pos"].tolist() == [2, 3, 4] and ep["gather"].tolist() == [2]
+
+
+def test_segment_mask_is_branch_mask_for_one_segment(orc):
+    for past, n in ((0, 7), (5, 4)):
+        assert np.array_equal(orc.segment_mask(np.zeros(n, np.uint32), past), orc.branch_mask(n, past))
+
+
+def _check_packed_equivalence(orc):
+    """Packed block b == causal attention over [prefix || block b] alone (qwen3.rs:13-17)."""
+    P, lens, d = 19, [5, 1, 7], 32
+    ep = orc.engine_pass([(P, P, P)], [(0, L) for L in lens])
+    n = ep["n"]
+    q = RNG.standard_normal((2, n, d)).astype(np.float32)
+    k = RNG.standard_normal((1, P + n, d)).astype(np.float32)
+    v = RNG.standard_normal((1, P + n, d)).astype(np.float32)
+    packed = orc.attend(q, k, v, ep["mask"], False)[0]
+    ok, r0 = True, 0
+    for L in lens:
+        kb = np.concatenate([k[:, :P], k[:, P + r0: P + r0 + L]], axis=1)
+        vb = np.concatenate([v[:, :P], v[:, P + r0: P + r0 + L]], axis=1)
+        alone = orc.attend(q[:, r0: r0 + L], kb, vb, orc.branch_mask(L, P), False)[0]
+        ok &= np.array_equal(packed[:, r0: r0 + L], alone)
+        r0 += L
+    return bool(ok)
+
+
+def test_packed_equals_each_block_alone(orc):
+    assert _check_packed_equivalence(orc)
+
+
+def test_packed_equivalence_catches_mask(orc):
+    with oracle.mutation(oracle.MUT_MASK_NO_DIAG):
+        assert not _check_packed_equivalence(orc)
+
+
+def test_sigmoid_gate_matches_closed_form(orc):
+    o = RNG.standard_normal(1000).astype(np.float32)
+    g = RNG.standard_normal(1000).astype(np.float32)
+    got = orc.sigmoid_gate(o, g, False)
+    assert np.abs(got - o / (1 + np.exp(-g.astype(np.float64)))).max() < 1e-6
+    gb = orc.sigmoid_gate(orc.round_bf16(o), orc.round_bf16(g), True)
+    assert np.abs(gb - o / (1 + np.exp(-g.astype(np.float64)))).max() < 2e-2
+
+
+# ---------------------------------------------------------------- Gated DeltaNet
+
+
+def _ref_gen(n, seed):
+    """The deterministic generator of the reference's test (qwen35.rs:781)."""
+    i = np.arange(n, dtype=np.uint64)
+    return (((i + 1) * np.uint64(seed + 7919)) % np.uint64(1000)).astype(np.float32) / np.float32(500.0) - np.float32(1.0)
+
+
+def _gdn_case(orc):
+    b, h, t, dk, dv = 1, 2, 70, 4, 3
+    q = _ref_gen(b * h * t * dk, 1).reshape(h, t, dk)
+    k = _ref_gen(b * h * t * dk, 2).reshape(h, t, dk)
+    v = _ref_gen(b * h * t * dv, 3).reshape(h, t, dv)
+    g = (np.abs(_ref_gen(b * h * t, 4)) * np.float32(-0.5)).reshape(h, t)
+    beta = (1.0 / (1.0 + np.exp(-_ref_gen(b * h * t, 5).astype(np.float64)))).astype(np.float32).reshape(h, t)
+    return q, k, v, g, beta
+
+
+def _check_gdn(orc):
+    q, k, v, g, beta = _gdn_case(orc)
+    out, s = orc.chunk_gated_delta_rule(q, k, v, g, beta)
+    dk = q.shape[-1]
+    qn = (orc.l2norm(q) * np.float32(dk ** -0.5)).astype(np.float32)
+    kn = orc.l2norm(k)
+    ro, rs = orc.gdn_recurrence(qn, kn, v, g, beta)
+    return bool(np.abs(out - ro).max() < 2e-4 and np.abs(s - rs).max() < 2e-4)
+
+
+def test_gdn_chunked_rule_matches_recurrence(orc):
+    """qwen35.rs:776-822 with the reference's generator and tolerance."""
+    assert _check_gdn(orc)
+
+
+def test_gdn_catches_missing_decay(orc):
+    with oracle.mutation(oracle.MUT_GDN_NO_DECAY):
+        assert not _check_gdn(orc)
+
+
+def test_gdn_with_initial_state_continues_the_sequence(orc):
+    q, k, v, g, beta = _gdn_case(orc)
+    full, s_full = orc.chunk_gated_delta_rule(q, k, v, g, beta)
+    a, s_a = orc.chunk_gated_delta_rule(q[:, :40], k[:, :40], v[:, :40], g[:, :40], beta[:, :40])
+    b, s_b = orc.chunk_gated_delta_rule(q[:, 40:], k[:, 40:], v[:, 40:], g[:, 40:], beta[:, 40:], s0=s_a)
+    assert np.abs(np.concatenate([a, b], 1) - full).max() < 2e-4
+    assert np.abs(s_b - s_full).max() < 2e-4
+
+
+def test_inv_unit_lower_matches_definition(orc):
+    """qwen35.rs:758-774: (I + strict_lower(m)) . inv == I."""
+    n = 8
+    vals = ((np.arange(n * n) * 37 % 11).astype(np.float32) - 5.0) / 7.0
+    m = vals.reshape(1, n, n).astype(np.float32)
+    inv = orc.inv_unit_lower(m)[0]
+    a = np.tril(m[0], -1) + np.eye(n, dtype=np.float32)
+    assert np.abs(a @ inv - np.eye(n)).max() < 1e-4
+    assert np.abs(inv - np.linalg.inv(a.astype(np.float64))).max() < 1e-4
+    big = RNG.standard_normal((3, 64, 64)).astype(np.float32) * 0.1
+    inv = orc.inv_unit_lower(big)
+    for i in range(3):
+        a = np.tril(big[i], -1) + np.eye(64)
+        assert np.abs(a @ inv[i] - np.eye(64)).max() < 1e-4
+
+
+def test_softplus_closed_form(orc):
+    for x in (-30.0, -2.0, 0.0, 0.5, 3.0, 40.0):
+        assert abs(orc.softplus(x) - math.log1p(math.exp(x)) if x < 30 else abs(orc.softplus(x) - x)) < 1e-5
