@@ -56,12 +56,12 @@ __device__ __forceinline__ int4 clamp_seg(int4 sg, int s_cache, int t) {
 __device__ __forceinline__ float gate_value(float o, float g, bool bf16) {
   // out * sigmoid(g), each op in the model dtype (qwen35.rs:556-558)
   if (bf16) {
-    float e = bf16_round(__expf(-g));
+    float e = bf16_round(expf(-g));
     float den = bf16_round(e + 1.0f);
     float sg = bf16_round(1.0f / den);
     return bf16_round(bf16_round(o) * sg);
   }
-  return o * (1.0f / (__expf(-g) + 1.0f));
+  return o * (1.0f / (expf(-g) + 1.0f));
 }
 
 // --------------------------------------------------------------------------

@@ -10,7 +10,9 @@
 //   y_e  = dtype(dtype(x_e / m) * w_e)
 //   rope: y_i = dtype(dtype(y_i c) - dtype(y_{i+h} s)), y_{i+h} = dtype(dtype(y_i s) + dtype(y_{i+h} c))
 // This file is compiled with -ffp-contract=off so no product is fused into
-// an add, as in the reference.
+// an add, as in the reference.  Plain `/` and sqrtf are the correctly
+// rounded HIP forms (hipcc's default); __fsqrt_rn is not (it maps to the
+// native approximate square root) and must not be used here.
 //
 // Work split: a wave normalises 8 vectors (token, head) at a time.  Lanes
 // load the 8 x D elements coalesced, the squares go through LDS and lanes
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(WAVES * 64) void qknorm_rope_kernel(QkArgs a) {
   if (lane < VPW) {
     float s = 0.0f;
     for (int e = 0; e < D; ++e) s += buf[wave][lane][e];
-    msh[wave][lane] = rnd(__fsqrt_rn(__fdiv_rn(s, (float)D) + a.eps));
+    msh[wave][lane] = rnd(sqrtf(s / (float)D + a.eps));
   }
   __syncthreads();
 #pragma unroll
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(WAVES * 64) void qknorm_rope_kernel(QkArgs a) {
       const int e = lane + 64 * k;
       float w = wgt[j] ? ld<T>(wgt[j], e) : 0.0f;
       if (a.plus_one) w = rnd(w + 1.0f);
-      const float y = rnd(rnd(__fdiv_rn(x[j][k], m)) * w);
+      const float y = rnd(rnd(x[j][k] / m) * w);
       x[j][k] = y;
       buf[wave][j][e] = y;
     }

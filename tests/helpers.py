@@ -6,6 +6,7 @@ import numpy as np
 
 import cev_hip
 from cev_hip import configs
+from cev_hip.layer import AttentionLayer, default_table  # noqa: F401
 
 
 def to_dev(x: np.ndarray, bf16: bool, device):
@@ -19,66 +20,7 @@ def to_np(t) -> np.ndarray:
     return t.detach().to(torch.float32).cpu().numpy()
 
 
-class GpuLayer:
-    """K1 (QK-norm + RoPE) then K2 (packed attention) for a workload, inputs
-    resident on the device."""
-
-    def __init__(self, w: configs.AttnWorkload, device, table=None, inputs=None):
-        import torch
-        self.w = w
-        self.dev = device
-        bf = w.bf16
-        self.dtype = torch.bfloat16 if bf else torch.float32
-        if inputs is None:
-            pk, pv = w.prefix_kv()
-            q, k, v = w.suffix_qkv()
-            wq, wk = w.norm_weights()
-        else:
-            pk, pv, q, k, v, wq, wk = inputs
-        self.np_inputs = (pk, pv, q, k, v, wq, wk)
-        self.pk = to_dev(pk, bf, device) if w.prefix else None
-        self.pv = to_dev(pv, bf, device) if w.prefix else None
-        self.qp = to_dev(q, bf, device)             # (t, hq, d) or gated (t, hq, 2d)
-        self.k_in = to_dev(k, bf, device)
-        self.v = to_dev(v, bf, device)
-        self.wq = to_dev(wq, bf, device)
-        self.wk = to_dev(wk, bf, device)
-        self.pos = torch.from_numpy(w.positions()).to(device)
-        self.rot = cev_hip.Rotary(w.theta, w.rotary_dim, w.n_pos(), self.dtype, device)
-        d = w.d
-        self.q_in = self.qp[:, :, :d]
-        self.gate = self.qp[:, :, d:] if w.gated else None
-        self.q = torch.empty((w.t, w.hq, d), dtype=self.dtype, device=device)
-        self.k = torch.empty((w.t, w.hkv, d), dtype=self.dtype, device=device)
-        self.out = torch.empty((w.t, w.hq, d), dtype=self.dtype, device=device)
-        if table is None:
-            table = default_table(w)
-        self.table = table
-        self.attn = cev_hip.PackedAttention(self.q, self.k, table, k_cache=self.pk, s_cache=w.prefix, has_gate=w.gated,
-                                            out=self.out, gate=self.gate, v_new=self.v, v_cache=self.pv)
-
-    def qknorm(self):
-        cev_hip.qknorm_rope(self.q_in, self.k_in, self.wq, self.wk, self.pos, self.rot, self.w.eps, plus_one=self.w.plus_one,
-                            q_out=self.q, k_out=self.k)
-
-    def attend(self):
-        return self.attn(self.q, self.k, self.v, self.pk, self.pv, self.gate, self.out)
-
-    def forward(self):
-        self.qknorm()
-        return self.attend()
-
-
-def default_table(w: configs.AttnWorkload) -> cev_hip.BlockTable:
-    if w.causal:
-        if w.prefix == 0:
-            return cev_hip.BlockTable.from_rows(len(w.blocks), w.blocks[0], 0, causal=True)
-        plans, items = w.plans_items()
-        tab, pos, _ = cev_hip.BlockTable.from_plans(plans, items)
-        assert np.array_equal(pos, w.positions())
-        return tab
-    assert len(set(w.blocks)) == 1
-    return cev_hip.BlockTable.from_rows(len(w.blocks), w.blocks[0], 0, causal=False, lengths=w.lengths)
+GpuLayer = AttentionLayer
 
 
 class OracleLayer:
