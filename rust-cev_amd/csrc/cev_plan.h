@@ -25,7 +25,8 @@ struct cev_plan_header {
 static_assert(sizeof(cev_plan_header) == 64, "plan header is 64 bytes");
 
 // Waves per workgroup and query rows per tile for a GQA group size g:
-// every wave owns 32 rows of one query head, the waves of a workgroup cover
-// all g heads of one KV head, so each staged K/V tile feeds g x rows queries.
-static inline int cev_attn_waves(int g) { return g <= 1 ? 2 : (g == 2 ? 4 : 8); }
-static inline int cev_attn_tile_rows(int g) { return 32 * cev_attn_waves(g) / g; }
+// every wave owns 32 rows of one query head, the 8 waves of a workgroup
+// cover all g heads of one KV head, so each staged K/V tile feeds 256
+// queries (g heads x 256/g rows).
+constexpr int kAttnWaves = 8;
+static inline int cev_attn_tile_rows(int g) { return 32 * kAttnWaves / g; }
