@@ -111,6 +111,13 @@ typedef struct {
   int64_t vn_stride_t, vn_stride_h;
   int64_t g_stride_t, g_stride_h;
   int64_t o_stride_t, o_stride_h;
+  /* Key-range splitting: 0 lets the planner choose (split a tile's keys
+   * over several workgroups when there are too few tiles to fill the GPU),
+   * 1 disables it, n > 1 caps the parts per tile at n.  Split parts write
+   * partial results to the workspace and a merge pass combines them, so
+   * results can differ from an unsplit run in the last bits. */
+  int32_t max_splits;
+  int32_t reserved;
 } cev_attn_desc;
 
 /* Fills `d` with dense strides for the layouts above (token-major q, gate,
@@ -128,12 +135,17 @@ int32_t cev_attn_desc_init(cev_attn_desc* d, int32_t dtype, int32_t n_q_heads, i
 int32_t cev_attn_plan_size(const cev_attn_desc* d, const cev_block* blocks, int32_t n_blocks, size_t* bytes);
 int32_t cev_attn_plan_build(const cev_attn_desc* d, const cev_block* blocks, int32_t n_blocks, void* plan, size_t bytes);
 
+/* Device workspace bytes a plan needs (0 when no tile is split). */
+int32_t cev_attn_workspace_size(const void* plan_host, size_t* bytes);
+
 /* Packed-prefill attention: replaces Attention::attend
  * (qwen3.rs:206-220, qwen35.rs:563-579) plus the output gate of
  * qwen35.rs:556-558 when has_gate.  k_cache/v_cache may be NULL when
- * s_cache == 0, gate NULL when !has_gate. */
+ * s_cache == 0, gate NULL when !has_gate, workspace NULL when the plan
+ * needs none.  Calls sharing one workspace must not overlap. */
 int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q, const void* k_cache,
-                             const void* v_cache, const void* k_new, const void* v_new, const void* gate, void* out, cev_stream stream);
+                             const void* v_cache, const void* k_new, const void* v_new, const void* gate, void* out, void* workspace,
+                             size_t workspace_bytes, cev_stream stream);
 
 /* ------------------------------------------------------------------ */
 /* Fused QK RMSNorm + RoPE with per-token positions: replaces

@@ -167,23 +167,39 @@ class AttnPlan:
         off = (-raw.ctypes.data) % 16
         self.host = raw[off: off + size.value]
         check(L.cev_attn_plan_build(C.byref(desc), arr, len(table), C.c_void_p(self.host.ctypes.data), size.value))
-        hdr = self.host[:64].view(np.int32)
+        hdr = self.header()
         self.n_tiles = int(hdr[2])
         self.n_segs = int(hdr[3])
         self.tile_rows = int(hdr[6])
+        self.n_splits = int(hdr[15])
+        self.block_n = int(hdr[16])
         self.nbytes = size.value
+        ws = C.c_size_t()
+        check(L.cev_attn_workspace_size(C.c_void_p(self.host.ctypes.data), C.byref(ws)))
+        self.workspace_bytes = ws.value
         self.dev = None
+        self.workspace = None
         if device is not None:
             torch = _torch()
             self.dev = torch.from_numpy(self.host.copy()).to(device)
+            if self.workspace_bytes:
+                self.workspace = torch.empty(self.workspace_bytes, dtype=torch.uint8, device=device)
+
+    def header(self) -> np.ndarray:
+        return self.host[:80].view(np.int32)
 
     def tiles(self) -> np.ndarray:
-        hdr = self.host[:64].view(np.int32)
-        return self.host.view(np.int32)[hdr[11]: hdr[11] + 4 * self.n_tiles].reshape(-1, 4)
+        """(n_tiles, 8): row_begin, row_count, seg_begin, seg_count, n_chunks, 0, 0, 0."""
+        hdr = self.header()
+        return self.host.view(np.int32)[hdr[11]: hdr[11] + 8 * self.n_tiles].reshape(-1, 8)
 
     def segs(self) -> np.ndarray:
-        hdr = self.host[:64].view(np.int32)
+        hdr = self.header()
         return self.host.view(np.int32)[hdr[12]: hdr[12] + 4 * self.n_segs].reshape(-1, 4)
+
+    def rows(self) -> np.ndarray:
+        hdr = self.header()
+        return self.host.view(np.int32)[hdr[13]: hdr[13] + 4 * int(hdr[4])].reshape(-1, 4)
 
 
 class PackedAttention:
@@ -194,13 +210,14 @@ class PackedAttention:
     k_cache / v_cache (hkv, s_cache, d); k_new / v_new (t, hkv, d)."""
 
     def __init__(self, q, k_new, table: BlockTable, k_cache=None, s_cache: int = 0, has_gate: bool = False,
-                 scale: Optional[float] = None, out=None, gate=None, v_new=None, v_cache=None):
+                 scale: Optional[float] = None, out=None, gate=None, v_new=None, v_cache=None, max_splits: int = 0):
         t, hq, d = q.shape
         hkv = k_new.shape[1]
         if table.t != t or table.s_cache != s_cache:
             raise CevError(-1, f"table is for t={table.t}, s_cache={table.s_cache}; call has t={t}, s_cache={s_cache}")
         self.dtype = _dtype_code(q)
         self.desc = attn_desc(self.dtype, hq, hkv, d, t, s_cache, has_gate, scale)
+        self.desc.max_splits = int(max_splits)
         self._set_strides(q, k_new, v_new if v_new is not None else k_new, k_cache, v_cache if v_cache is not None else k_cache,
                           out if out is not None else q, gate)
         self.plan = AttnPlan(self.desc, table, device=q.device)
@@ -227,14 +244,15 @@ class PackedAttention:
         self._set_strides(q, k_new, v_new, k_cache, v_cache, out, gate)
         check(lib().cev_packed_attention(C.byref(self.desc), C.c_void_p(self.plan.host.ctypes.data), _ptr(self.plan.dev), _ptr(q),
                                          _ptr(k_cache), _ptr(v_cache), _ptr(k_new), _ptr(v_new), _ptr(gate), _ptr(out),
-                                         _stream_ptr(stream)))
+                                         _ptr(self.plan.workspace), self.plan.workspace_bytes, _stream_ptr(stream)))
         return out
 
 
-def packed_attention(q, k_new, v_new, table: BlockTable, k_cache=None, v_cache=None, gate=None, scale=None, out=None, stream=None):
+def packed_attention(q, k_new, v_new, table: BlockTable, k_cache=None, v_cache=None, gate=None, scale=None, out=None, stream=None,
+                     max_splits: int = 0):
     s_cache = 0 if k_cache is None else k_cache.shape[1]
     op = PackedAttention(q, k_new, table, k_cache=k_cache, s_cache=s_cache, has_gate=gate is not None, scale=scale, out=out,
-                         gate=gate, v_new=v_new, v_cache=v_cache)
+                         gate=gate, v_new=v_new, v_cache=v_cache, max_splits=max_splits)
     return op(q, k_new, v_new, k_cache, v_cache, gate, out, stream)
 
 

@@ -56,6 +56,7 @@ class AttnDesc(C.Structure):
         ("vn_stride_t", i64), ("vn_stride_h", i64),
         ("g_stride_t", i64), ("g_stride_h", i64),
         ("o_stride_t", i64), ("o_stride_h", i64),
+        ("max_splits", i32), ("reserved", i32),
     ]
 
 
@@ -80,7 +81,8 @@ SIGNATURES = {
     "cev_attn_desc_init": (i32, [C.POINTER(AttnDesc), i32, i32, i32, i32, i32, i32, i32]),
     "cev_attn_plan_size": (i32, [C.POINTER(AttnDesc), PBlock, i32, C.POINTER(C.c_size_t)]),
     "cev_attn_plan_build": (i32, [C.POINTER(AttnDesc), PBlock, i32, P, C.c_size_t]),
-    "cev_packed_attention": (i32, [C.POINTER(AttnDesc), P, P, P, P, P, P, P, P, P, P]),
+    "cev_attn_workspace_size": (i32, [P, C.POINTER(C.c_size_t)]),
+    "cev_packed_attention": (i32, [C.POINTER(AttnDesc), P, P, P, P, P, P, P, P, P, P, C.c_size_t, P]),
     "cev_qknorm_desc_init": (i32, [C.POINTER(QkNormDesc), i32, i32, i32, i32, i32, i32, i32, i32, C.c_float, i32]),
     "cev_qknorm_rope": (i32, [C.POINTER(QkNormDesc), P, P, P, P, P, P, P, P, P, P]),
     "cev_rope_table": (i32, [C.c_double, i32, i32, i32, P, P]),

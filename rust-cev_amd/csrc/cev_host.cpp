@@ -206,7 +206,7 @@ bool same_spans(const cev_block& a, const cev_block& b) {
 
 struct Plan {
   std::vector<int32_t> tiles, segs, rows;
-  int32_t n_tiles = 0, n_segs = 0, tile_rows = 0;
+  int32_t n_tiles = 0, n_segs = 0, tile_rows = 0, n_splits = 1, block_n = 0;
 };
 
 void push_seg(Plan& p, int32_t b, int32_t e, int32_t masked, int32_t s_cache) {
@@ -230,8 +230,10 @@ int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, P
   if (rc) return rc;
   rc = check_blocks(d, blocks, n);
   if (rc) return rc;
+  CEV_CHECK_ARG(d->max_splits >= 0, "max_splits %d < 0", d->max_splits);
   const int g = d->n_q_heads / d->n_kv_heads;
   p.tile_rows = cev_attn_tile_rows(g);
+  p.block_n = cev_attn_block_n(d->dtype, d->head_dim);
   p.rows.assign((size_t)d->t * 4, 0);
   std::vector<int32_t> owner((size_t)d->t, -1);
   for (int32_t i = 0; i < d->t; ++i) p.rows[(size_t)i * 4 + 2] = -1;
@@ -301,11 +303,31 @@ int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, P
           push_seg(p, u.b, u.e, 1, d->s_cache);
         }
       }
-      p.tiles.insert(p.tiles.end(), {tr, te - tr, seg_begin, p.n_segs - seg_begin});
+      int32_t chunks = 0;
+      for (int32_t si = seg_begin; si < p.n_segs; ++si) {
+        const int32_t len = p.segs[(size_t)si * 4 + 1] - p.segs[(size_t)si * 4];
+        chunks += (len + p.block_n - 1) / p.block_n;
+      }
+      p.tiles.insert(p.tiles.end(), {tr, te - tr, seg_begin, p.n_segs - seg_begin, chunks, 0, 0, 0});
       p.n_tiles++;
     }
     oi = oj;
   }
+  // Split the key stream of every tile when the tiles alone leave the GPU
+  // underfilled (few long-prefix rows): each part still gets at least
+  // kSplitMinChunks key tiles.
+  int32_t max_chunks = 0;
+  for (int32_t ti = 0; ti < p.n_tiles; ++ti) max_chunks = std::max(max_chunks, p.tiles[(size_t)ti * 8 + 4]);
+  const int64_t items = (int64_t)p.n_tiles * d->n_kv_heads;
+  int64_t split = 1;
+  if (items > 0 && d->max_splits != 1) {
+    split = (kSplitTargetWorkgroups + items - 1) / items;
+    split = std::min<int64_t>(split, std::max(1, max_chunks / kSplitMinChunks));
+    split = std::min<int64_t>(split, kSplitMax);
+    if (d->max_splits > 1) split = std::min<int64_t>(split, d->max_splits);
+    split = std::max<int64_t>(split, 1);
+  }
+  p.n_splits = (int32_t)split;
   return CEV_OK;
 }
 
@@ -348,11 +370,21 @@ extern "C" int32_t cev_attn_plan_build(const cev_attn_desc* d, const cev_block* 
   h.segs_off = h.tiles_off + (int32_t)p.tiles.size();
   h.rows_off = h.segs_off + (int32_t)p.segs.size();
   h.bytes = (int32_t)need;
+  h.n_splits = p.n_splits;
+  h.block_n = p.block_n;
   int32_t* out = (int32_t*)plan;
   memcpy(out, &h, sizeof h);
   if (!p.tiles.empty()) memcpy(out + h.tiles_off, p.tiles.data(), 4 * p.tiles.size());
   if (!p.segs.empty()) memcpy(out + h.segs_off, p.segs.data(), 4 * p.segs.size());
   if (!p.rows.empty()) memcpy(out + h.rows_off, p.rows.data(), 4 * p.rows.size());
+  return CEV_OK;
+}
+
+extern "C" int32_t cev_attn_workspace_size(const void* plan_host, size_t* bytes) {
+  CEV_CHECK_ARG(plan_host != nullptr && bytes != nullptr, "cev_attn_workspace_size: null argument");
+  const cev_plan_header* h = (const cev_plan_header*)plan_host;
+  CEV_CHECK_ARG(h->magic == CEV_PLAN_MAGIC && h->version == CEV_PLAN_VERSION, "cev_attn_workspace_size: not a plan");
+  *bytes = h->n_splits > 1 ? (size_t)h->t * h->n_q_heads * h->n_splits * cev_attn_partial_floats(h->head_dim) * sizeof(float) : 0;
   return CEV_OK;
 }
 

@@ -3,30 +3,56 @@
 //
 // Layout (all int32, 16-byte aligned sections):
 //   header                 16 x int32
-//   tiles[n_tiles]         {row_begin, row_count, seg_begin, seg_count}
+//   tiles[n_tiles]         {row_begin, row_count, seg_begin, seg_count,
+//                           n_chunks, 0, 0, 0}
 //   segs[n_segs]           {key_begin, key_end, masked, 0}   global key index, end exclusive
 //   rows[t]                {lo, hi, diag, 0}                 local keys a row sees:
 //                          [lo, hi) plus diag (diag < 0: none)
 // A tile is a run of query rows whose blocks share their span list; its
 // segments are the spans (unmasked) and its rows' local keys (masked where
-// not every row of the tile sees them).  No segment crosses s_cache.
+// not every row of the tile sees them).  No segment crosses s_cache.  A
+// tile's keys are visited in key tiles of block_n keys (n_chunks of them);
+// with n_splits > 1 each tile's chunks are cut into n_splits contiguous
+// parts, one workgroup per (tile, part, kv head).
 #pragma once
 #include <stdint.h>
 
+#if defined(__HIPCC__)
+#define CEV_HD __host__ __device__
+#else
+#define CEV_HD
+#endif
+
 #define CEV_PLAN_MAGIC 0x50564543  // "CEVP"
-#define CEV_PLAN_VERSION 1
+#define CEV_PLAN_VERSION 2
 
 struct cev_plan_header {
   int32_t magic, version, n_tiles, n_segs;
   int32_t t, s_cache, tile_rows, dtype;
   int32_t head_dim, n_q_heads, n_kv_heads, tiles_off;  // offsets in int32 units
-  int32_t segs_off, rows_off, bytes, reserved;
+  int32_t segs_off, rows_off, bytes, n_splits;
+  int32_t block_n, reserved[3];
 };
-static_assert(sizeof(cev_plan_header) == 64, "plan header is 64 bytes");
+static_assert(sizeof(cev_plan_header) == 80, "plan header is 80 bytes");
 
 // Waves per workgroup and query rows per tile for a GQA group size g:
 // every wave owns 32 rows of one query head, the 8 waves of a workgroup
 // cover all g heads of one KV head, so each staged K/V tile feeds 256
 // queries (g heads x 256/g rows).
 constexpr int kAttnWaves = 8;
-static inline int cev_attn_tile_rows(int g) { return 32 * kAttnWaves / g; }
+CEV_HD static inline int cev_attn_tile_rows(int g) { return 32 * kAttnWaves / g; }
+
+// Keys per LDS key tile: 64 for bf16 d=128, 32 otherwise (LDS and
+// register budget of the two head dims and of f32).
+CEV_HD static inline int cev_attn_block_n(int dtype, int head_dim) { return (dtype == 1 && head_dim == 128) ? 64 : 32; }
+
+// Per-(row, head, part) partial record in the split workspace: the
+// unnormalised output (head_dim floats), then the running max m (log2
+// units) and the sum l, padded to keep records 16-byte aligned.
+CEV_HD static inline int64_t cev_attn_partial_floats(int head_dim) { return (int64_t)head_dim + 4; }
+
+// Split policy: aim for this many workgroups, never cut a tile's key
+// stream into parts of fewer than kSplitMinChunks key tiles.
+constexpr int kSplitTargetWorkgroups = 512;
+constexpr int kSplitMinChunks = 4;
+constexpr int kSplitMax = 256;

@@ -2,22 +2,27 @@
 // (crates/cev-model/src/qwen3.rs:206-220, crates/cev-model/src/qwen35.rs:563-579)
 // with the block-offset table in place of the dense mask.
 //
-// Design (one workgroup = one tile of query rows x one KV head):
-//   - the waves of a workgroup own 32 query rows of one query head each and
-//     together cover every query head of the KV head's GQA group, so a K/V
-//     key tile staged in LDS once is scored by g x rows queries;
+// Design (one workgroup = one tile of query rows x one KV head [x one part
+// of the tile's key stream when it is split]):
+//   - the 8 waves x 32 query slots of a workgroup hold 256/g rows x the g
+//     query heads of one KV head's GQA group (slot -> row slot/g, head
+//     slot%g), so a K/V key tile staged in LDS once is scored by 256 queries;
 //   - scores are computed transposed, S^T = K . Q^T, on 32x32 MFMA tiles: a
 //     lane then holds 16 keys of ONE query row, and the softmax row max and
-//     row sum reduce inside the lane plus one exchange with the lane 32 away;
-//   - online softmax in base 2 (exp2 of q.k * scale * log2 e), f32 state;
-//   - O^T = V^T . P^T accumulates on MFMA: P stays in registers as the B
-//     operand (its K slots follow the S^T register order) and V is staged
-//     transposed in LDS so each lane reads 4-key runs;
+//     row sum reduce inside the lane plus one permlane32 swap;
+//   - online softmax in base 2 (exp2(q.k * scale * log2 e - m)), f32 state,
+//     O rescaled only when a row max grows by more than 2^kRescale;
+//   - O^T = V^T . P^T accumulates on MFMA with P kept in registers as the B
+//     operand (its K slots follow the S^T register order);
+//   - K/V key tiles are double-buffered in LDS: the next tile's global loads
+//     are in flight while the current one is scored;
 //   - the key ranges a tile visits come from the plan: spans are unmasked,
 //     local keys are masked per row from the row's [lo, hi) + diag;
-//   - blockIdx -> (tile, kv head) with the kv head fastest, so consecutive
-//     workgroups (spread round-robin over the 8 XCDs) of one XCD share a KV
-//     head and its K/V stream stays in that XCD's L2.
+//   - blockIdx -> (tile, part, kv head) with the kv head fastest, so the
+//     workgroups of one XCD (dispatched round-robin over the 8 XCDs) share a
+//     KV head and its K/V stream stays in that XCD's L2;
+//   - a split tile writes (unnormalised O, m, l) per row and head to the
+//     workspace and attn_merge_kernel combines the parts.
 #include "cev_device.h"
 #include "cev_internal.h"
 #include "cev_plan.h"
@@ -32,17 +37,20 @@ struct AttnArgs {
   const void* vn;
   const void* gate;
   void* out;
+  float* ws;
   const int32_t* plan;
   int64_t q_st, q_sh, kc_ss, kc_sh, vc_ss, vc_sh, kn_st, kn_sh, vn_st, vn_sh, g_st, g_sh, o_st, o_sh;
-  int32_t n_tiles, t, s_cache, hkv, g, has_gate;
+  int32_t n_tiles, t, s_cache, hq, hkv, g, has_gate, n_splits, tile_rows;
   float scale_log2;
 };
+
+constexpr float kRescale = 8.0f;
 
 // The plan header on the device must describe the launch; anything else
 // (a plan not copied from the host plan) makes every workgroup exit.
 __device__ __forceinline__ bool plan_ok(const AttnArgs& a) {
   const cev_plan_header* h = (const cev_plan_header*)a.plan;
-  return h->magic == CEV_PLAN_MAGIC && h->n_tiles == a.n_tiles && h->t == a.t && h->s_cache == a.s_cache;
+  return h->magic == CEV_PLAN_MAGIC && h->n_tiles == a.n_tiles && h->t == a.t && h->s_cache == a.s_cache && h->n_splits == a.n_splits;
 }
 
 // Clamps a segment to the key buffer it starts in.
@@ -64,31 +72,6 @@ __device__ __forceinline__ float gate_value(float o, float g, bool bf16) {
   return o * (1.0f / (expf(-g) + 1.0f));
 }
 
-// --------------------------------------------------------------------------
-// bf16: QK^T and PV on v_mfma_f32_32x32x16_bf16.
-//
-// Per key tile of BN keys (double-buffered in LDS, the next tile's global
-// loads in flight while this one is scored):
-//   S^T = K . Q^T                  16 x (D/16) MFMAs per wave
-//   row max on raw scores          lane-local + one permlane32 swap
-//   lazy rescale                   O and l are rescaled only when a row's max
-//                                  grows by more than 2^kRescale, so
-//                                  exp2(s*c - m) <= 2^kRescale in between
-//   P = exp2(fma(s, c, -m))        c = scale * log2(e)
-//   O^T += V^T . P^T               V stays key-major in LDS; the A operand
-//                                  (4 keys x 1 head-dim column per read) comes
-//                                  from ds_read_b64_tr_b16, the gfx950 LDS
-//                                  transpose load.
-constexpr float kRescale = 8.0f;
-constexpr int kPad = 8;  // bf16 elements of padding per LDS row
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ bf16x4 lds_read_tr(const __bf16* p) {
-  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
-  return __builtin_bit_cast(bf16x4, r);
-}
-
 __device__ __forceinline__ float pair_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -99,49 +82,185 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// A position in a tile's key stream: segment si, key offset k0 within it.
-struct Cursor {
-  int si, k0;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x4 lds_read_tr(const __bf16* p) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(bf16x4, r);
+}
+
+// --------------------------------------------------------------------------
+// Per-dtype MFMA fragments.
+//
+// bf16 (v_mfma_f32_32x32x16_bf16): Q as the B operand, 8 head-dim values per
+// lane per step; P converted to bf16 B operands whose K slot 8u + j of half
+// h is S^T register 8h + j (key 16h + 8(j/4) + 4u + j%4 of a sub-tile); the
+// V^T A operand comes from ds_read_b64_tr_b16 on the key-major V tile.
+//
+// f32 (v_mfma_f32_32x32x2_f32, full f32 products): the head-dim order of
+// the QK^T K slots is permuted (d = 8k + 4u + r) so a lane reads 4
+// consecutive floats for 4 steps; one K=2 PV step per S^T register.
+template <typename T, int D>
+struct Frag;
+
+template <int D>
+struct Frag<__bf16, D> {
+  static constexpr int BN = D == 128 ? 64 : 32;
+  static constexpr int PAD = 8;
+  static constexpr int VEC = 8;
+  typedef bf16x8 Vec;
+  bf16x8 q[D / 16];
+
+  __device__ __forceinline__ void load_q(const __bf16* qp, bool ok, int u) {
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      bf16x8 z = {};
+      q[s] = ok ? *(const bf16x8*)(qp + 16 * s + 8 * u) : z;
+    }
+  }
+
+  template <int RS>
+  __device__ __forceinline__ f32x16 qk(const __bf16* sK, int kt, int n, int u) const {
+    f32x16 s = {};
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) {
+      const bf16x8 af = *(const bf16x8*)&sK[(kt * 32 + n) * RS + 16 * st + 8 * u];
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, q[st], s, 0, 0, 0);
+    }
+    return s;
+  }
+
+  // o[dt] += V^T . P^T for one 32-key sub-tile kt whose probabilities are p.
+  template <int RS>
+  __device__ __forceinline__ void pv(const __bf16* sV, int kt, int lane, int u, const f32x16& p, f32x16* o) const {
+    bf16x8 pf[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pf[h][j] = (__bf16)p[8 * h + j];
+    // Lane (group g16 = lane/16, i = lane%16) reads row kb + i/4, columns
+    // d0 + 4(i%4) .. +3; the transpose load hands it 4 consecutive keys of
+    // head-dim column d0 + i.
+    const int tr_row = (lane & 15) >> 2;
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const __bf16* vp = sV + (kt * 32 + 16 * h + 4 * u + tr_row) * RS + dt * 32 + tr_col;
+        const bf16x4 lo = lds_read_tr(vp);
+        const bf16x4 hi = lds_read_tr(vp + 8 * RS);
+        const bf16x8 af = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[h], o[dt], 0, 0, 0);
+      }
+  }
 };
 
-template <int D, int BN>
-__global__ __launch_bounds__(kAttnWaves * 64) void attn_bf16_kernel(AttnArgs a) {
+template <int D>
+struct Frag<float, D> {
+  static constexpr int BN = 32;
+  static constexpr int PAD = 4;
+  static constexpr int VEC = 4;
+  typedef f32x4 Vec;
+  f32x4 q[D / 8];
+
+  __device__ __forceinline__ void load_q(const float* qp, bool ok, int u) {
+#pragma unroll
+    for (int k = 0; k < D / 8; ++k) q[k] = ok ? *(const f32x4*)(qp + 8 * k + 4 * u) : f32x4{};
+  }
+
+  template <int RS>
+  __device__ __forceinline__ f32x16 qk(const float* sK, int kt, int n, int u) const {
+    f32x16 s = {};
+#pragma unroll
+    for (int k = 0; k < D / 8; ++k) {
+      const f32x4 af = *(const f32x4*)&sK[(kt * 32 + n) * RS + 8 * k + 4 * u];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s = __builtin_amdgcn_mfma_f32_32x32x2f32(af[r], q[k][r], s, 0, 0, 0);
+    }
+    return s;
+  }
+
+  template <int RS>
+  __device__ __forceinline__ void pv(const float* sV, int kt, int lane, int u, const f32x16& p, f32x16* o) const {
+    const int n = lane & 31;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(sV[key * RS + dt * 32 + n], p[i], o[dt], 0, 0, 0);
+    }
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ void store_vec4(T* p, const float* v);
+template <>
+__device__ __forceinline__ void store_vec4<__bf16>(__bf16* p, const float* v) {
+  bf16x4 r = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+  *(bf16x4*)p = r;
+}
+template <>
+__device__ __forceinline__ void store_vec4<float>(float* p, const float* v) {
+  *(f32x4*)p = f32x4{v[0], v[1], v[2], v[3]};
+}
+
+template <typename T>
+__device__ __forceinline__ void load_vec4(const T* p, float* v);
+template <>
+__device__ __forceinline__ void load_vec4<__bf16>(const __bf16* p, float* v) {
+  const bf16x4 g = *(const bf16x4*)p;
+  for (int e = 0; e < 4; ++e) v[e] = (float)g[e];
+}
+template <>
+__device__ __forceinline__ void load_vec4<float>(const float* p, float* v) {
+  const f32x4 g = *(const f32x4*)p;
+  for (int e = 0; e < 4; ++e) v[e] = g[e];
+}
+
+// --------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
+  using F = Frag<T, D>;
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int BN = F::BN;
   constexpr int NT = kAttnWaves * 64;
-  constexpr int RS = D + kPad;    // LDS row stride (elements) of K and V tiles
+  constexpr int VEC = F::VEC;
+  constexpr int RS = D + F::PAD;  // LDS row stride (elements) of K and V tiles
   constexpr int TILE = BN * RS;   // one K or V tile
   constexpr int NKT = BN / 32;    // 32-key sub-tiles per key tile
   constexpr int NDT = D / 32;     // 32-wide slices of the head dim
-  constexpr int NQS = D / 16;     // K=16 steps over the head dim
-  constexpr int NLD = BN * D / 8 / NT;  // 16-byte loads per thread per tensor
-  static_assert(BN * D / 8 % NT == 0, "tile loads must split evenly");
-  __shared__ __align__(16) __bf16 smem[2 * 2 * TILE];
+  constexpr int NLD = BN * D / VEC / NT;  // 16-byte loads per thread per tensor
+  static_assert(BN * D / VEC % NT == 0, "tile loads must split evenly");
+  typedef typename F::Vec Vec;
+  __shared__ __align__(16) T smem[2 * 2 * TILE];
 
   if (!plan_ok(a)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, u = lane >> 5;
   const int kvh = blockIdx.x % a.hkv;
-  const int tile = blockIdx.x / a.hkv;
+  const int item = blockIdx.x / a.hkv;
+  const int tile = item / a.n_splits, part = item % a.n_splits;
   const cev_plan_header* ph = (const cev_plan_header*)a.plan;
-  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[tile];
+  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[2 * tile];
+  const int n_chunks = ((const int4*)(a.plan + ph->tiles_off))[2 * tile + 1].x;
   const int4* segs = (const int4*)(a.plan + ph->segs_off) + td.z;
   const int nseg = td.w;
   const int4* rows = (const int4*)(a.plan + ph->rows_off);
-  const int gi = wave % a.g, rg = wave / a.g;
+  // Query slot (wave, n) holds row slot / g of the tile, query head slot % g:
+  // the valid rows of a short tile fill the first waves, and a wave with no
+  // valid row skips the MFMA work (it still helps stage K/V).
+  const int slot = wave * 32 + n;
+  const int gi = slot % a.g;
   const int head = kvh * a.g + gi;
-  const int rit = rg * 32 + n;
+  const int rit = slot / a.g;
   const bool row_ok = rit < td.y && td.x + rit < a.t;
   const int row = row_ok ? td.x + rit : 0;
+  const bool wave_active = (wave * 32) / a.g < td.y;
   const float c = a.scale_log2;
 
-  bf16x8 qf[NQS];
-  {
-    const __bf16* qp = (const __bf16*)a.q + (int64_t)row * a.q_st + (int64_t)head * a.q_sh;
-#pragma unroll
-    for (int s = 0; s < NQS; ++s) {
-      bf16x8 z = {};
-      qf[s] = row_ok ? *(const bf16x8*)(qp + 16 * s + 8 * u) : z;
-    }
-  }
+  F fr;
+  fr.load_q((const T*)a.q + (int64_t)row * a.q_st + (int64_t)head * a.q_sh, row_ok, u);
   int4 rv = rows[row];
   if (!row_ok) rv = make_int4(0, 0, -1, 0);
 
@@ -150,92 +269,92 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_bf16_kernel(AttnArgs a) 
   for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
   float m_run = -1e30f, l_run = 0.0f;
 
-  // ---- key stream
-  auto seg_of = [&](int si) { return clamp_seg(segs[si], a.s_cache, a.t); };
-  auto first = [&](Cursor& cu) {
-    cu.si = 0;
-    cu.k0 = 0;
-    while (cu.si < nseg) {
-      const int4 sg = seg_of(cu.si);
-      if (sg.y > sg.x) return;
-      ++cu.si;
+  // ---- this part's slice of the tile's key stream: chunks [c0, c1)
+  const int c0 = (int)((int64_t)part * n_chunks / a.n_splits);
+  const int c1 = (int)((int64_t)(part + 1) * n_chunks / a.n_splits);
+  auto seg_of = [&](int s_i) { return clamp_seg(segs[s_i], a.s_cache, a.t); };
+  int si = 0, k0 = 0;
+  {
+    int cc = c0;
+    for (; si < nseg; ++si) {
+      const int4 sg = seg_of(si);
+      const int nch = (max(0, sg.y - sg.x) + BN - 1) / BN;
+      if (cc < nch) {
+        k0 = cc * BN;
+        break;
+      }
+      cc -= nch;
     }
-  };
-  auto advance = [&](Cursor& cu) {
-    const int4 sg = seg_of(cu.si);
-    cu.k0 += BN;
-    if (sg.x + cu.k0 < sg.y) return;
-    cu.k0 = 0;
-    for (++cu.si; cu.si < nseg; ++cu.si) {
-      const int4 s2 = seg_of(cu.si);
+  }
+  auto next = [&](int& s_i, int& s_k0) {
+    const int4 sg = seg_of(s_i);
+    s_k0 += BN;
+    if (sg.x + s_k0 < sg.y) return;
+    s_k0 = 0;
+    for (++s_i; s_i < nseg; ++s_i) {
+      const int4 s2 = seg_of(s_i);
       if (s2.y > s2.x) return;
     }
   };
-  bf16x8 kreg[NLD], vreg[NLD];
-  auto load = [&](const Cursor& cu) {
-    const int4 sg = seg_of(cu.si);
-    const int key0 = sg.x + cu.k0;
+
+  Vec kreg[NLD], vreg[NLD];
+  auto load = [&](int s_i, int s_k0) {
+    const int4 sg = seg_of(s_i);
+    const int key0 = sg.x + s_k0;
     const int nvalid = min(BN, sg.y - key0);
     const bool cached = key0 < a.s_cache;
-    const __bf16* kb = cached ? (const __bf16*)a.kc + kvh * a.kc_sh + (int64_t)key0 * a.kc_ss
-                              : (const __bf16*)a.kn + kvh * a.kn_sh + (int64_t)(key0 - a.s_cache) * a.kn_st;
-    const __bf16* vb = cached ? (const __bf16*)a.vc + kvh * a.vc_sh + (int64_t)key0 * a.vc_ss
-                              : (const __bf16*)a.vn + kvh * a.vn_sh + (int64_t)(key0 - a.s_cache) * a.vn_st;
+    const T* kb = cached ? (const T*)a.kc + kvh * a.kc_sh + (int64_t)key0 * a.kc_ss
+                         : (const T*)a.kn + kvh * a.kn_sh + (int64_t)(key0 - a.s_cache) * a.kn_st;
+    const T* vb = cached ? (const T*)a.vc + kvh * a.vc_sh + (int64_t)key0 * a.vc_ss
+                         : (const T*)a.vn + kvh * a.vn_sh + (int64_t)(key0 - a.s_cache) * a.vn_st;
     const int64_t ks = cached ? a.kc_ss : a.kn_st;
     const int64_t vs = cached ? a.vc_ss : a.vn_st;
 #pragma unroll
     for (int r = 0; r < NLD; ++r) {
       const int v = tid + r * NT;
-      const int key = v / (D / 8), col = (v % (D / 8)) * 8;
-      bf16x8 x = {}, y = {};
-      if (key < nvalid) {
-        x = *(const bf16x8*)(kb + (int64_t)key * ks + col);
-        y = *(const bf16x8*)(vb + (int64_t)key * vs + col);
+      const int key = v / (D / VEC), col = (v % (D / VEC)) * VEC;
+      Vec x = {}, y = {};
+      if (key < nvalid) {  // keys past the segment stay zero
+        x = *(const Vec*)(kb + (int64_t)key * ks + col);
+        y = *(const Vec*)(vb + (int64_t)key * vs + col);
       }
       kreg[r] = x;
       vreg[r] = y;
     }
   };
   auto store = [&](int buf) {
-    __bf16* sk = smem + buf * 2 * TILE;
+    T* sk = smem + buf * 2 * TILE;
 #pragma unroll
     for (int r = 0; r < NLD; ++r) {
       const int v = tid + r * NT;
-      const int key = v / (D / 8), col = (v % (D / 8)) * 8;
-      *(bf16x8*)&sk[key * RS + col] = kreg[r];
-      *(bf16x8*)&sk[TILE + key * RS + col] = vreg[r];
+      const int key = v / (D / VEC), col = (v % (D / VEC)) * VEC;
+      *(Vec*)&sk[key * RS + col] = kreg[r];
+      *(Vec*)&sk[TILE + key * RS + col] = vreg[r];
     }
   };
 
-  Cursor cur;
-  first(cur);
-  if (cur.si < nseg) {
-    load(cur);
+  const int my_chunks = c1 - c0;
+  if (my_chunks > 0 && si < nseg) {
+    load(si, k0);
     store(0);
     __syncthreads();
     int buf = 0;
-    for (;;) {
-      Cursor nxt = cur;
-      advance(nxt);
-      const bool more = nxt.si < nseg;
-      if (more) load(nxt);  // in flight while this tile is scored
+    for (int ci = 0;; ++ci) {
+      int nsi = si, nk0 = k0;
+      next(nsi, nk0);
+      const bool more = ci + 1 < my_chunks && nsi < nseg;
+      if (more) load(nsi, nk0);  // in flight while this tile is scored
 
-      const __bf16* sK = smem + buf * 2 * TILE;
-      const __bf16* sV = sK + TILE;
-      const int4 sg = seg_of(cur.si);
-      const int key0 = sg.x + cur.k0;
+      const T* sK = smem + buf * 2 * TILE;
+      const T* sV = sK + TILE;
+      const int4 sg = seg_of(si);
+      const int key0 = sg.x + k0;
       const int nvalid = min(BN, sg.y - key0);
 
+      if (wave_active) {
       f32x16 s[NKT];
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt) {
-        s[kt] = f32x16{};
-#pragma unroll
-        for (int st = 0; st < NQS; ++st) {
-          const bf16x8 af = *(const bf16x8*)&sK[(kt * 32 + n) * RS + 16 * st + 8 * u];
-          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[st], s[kt], 0, 0, 0);
-        }
-      }
+      for (int kt = 0; kt < NKT; ++kt) s[kt] = fr.template qk<RS>(sK, kt, n, u);
       if (sg.z != 0 || nvalid < BN) {
         // Branch-free on purpose: a short-circuit && / || here gives every
         // element its own control flow, and hipcc 7.2 then reuses the score
@@ -266,231 +385,162 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_bf16_kernel(AttnArgs a) 
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
       }
-      // P as bf16 B operands: K slot 8u + j of half h holds S^T register
-      // 8h + j, i.e. key 16h + 8(j/4) + 4u + j%4 of the sub-tile.
-      bf16x8 pf[NKT][2];
       float rs = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float p = fast_exp2(__builtin_fmaf(s[kt][8 * h + j], c, -m_run));
-            rs += p;
-            pf[kt][h][j] = (__bf16)p;
-          }
+        for (int i = 0; i < 16; ++i) {
+          const float p = fast_exp2(__builtin_fmaf(s[kt][i], c, -m_run));
+          s[kt][i] = p;
+          rs += p;
+        }
       l_run += rs;
-      // O^T += V^T . P^T.  Lane (group g16 = lane/16, i = lane%16) reads row
-      // key0' + (i/4), columns d0 + 4(i%4) .. +3; the transpose load hands it
-      // 4 consecutive keys of head-dim column d0 + i.
-      const int tr_row = (lane & 15) >> 2;
-      const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            const __bf16* vp = sV + (kt * 32 + 16 * h + 4 * u + tr_row) * RS + dt * 32 + tr_col;
-            const bf16x4 lo = lds_read_tr(vp);
-            const bf16x4 hi = lds_read_tr(vp + 8 * RS);
-            const bf16x8 af = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[kt][h], o[dt], 0, 0, 0);
-          }
+      for (int kt = 0; kt < NKT; ++kt) fr.template pv<RS>(sV, kt, lane, u, s[kt], o);
+      }
 
       if (!more) break;
       store(buf ^ 1);  // that buffer was last read before the previous barrier
       __syncthreads();
       buf ^= 1;
-      cur = nxt;
+      si = nsi;
+      k0 = nk0;
     }
   }
 
   const float l = pair_sum(l_run);
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   if (!row_ok) return;
-  __bf16* op = (__bf16*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
-  const __bf16* gp = a.has_gate ? (const __bf16*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh : nullptr;
+  if (a.n_splits > 1) {
+    // Partial record: O unnormalised, then m and l.
+    float* rec = a.ws + (((int64_t)row * a.hq + head) * a.n_splits + part) * cev_attn_partial_floats(D);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = dt * 32 + 8 * q4 + 4 * u;
+        *(f32x4*)(rec + d) = f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
+      }
+    if (u == 0) *(f32x4*)(rec + D) = f32x4{m_run, l, 0.0f, 0.0f};
+    return;
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh : nullptr;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d = dt * 32 + 8 * q4 + 4 * u;
-      bf16x4 r;
-      bf16x4 gv = {};
-      if (gp) gv = *(const bf16x4*)(gp + d);
+      float v[4], gv[4];
+      if (gp) load_vec4<T>(gp + d, gv);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float x = o[dt][4 * q4 + e] * inv;
-        if (gp) x = gate_value(x, (float)gv[e], true);
-        r[e] = (__bf16)x;
+        float x = BF ? o[dt][4 * q4 + e] * inv : (l > 0.0f ? o[dt][4 * q4 + e] / l : 0.0f);
+        if (gp) x = gate_value(x, gv[e], BF);
+        v[e] = x;
       }
-      *(bf16x4*)(op + d) = r;
+      store_vec4<T>(op + d, v);
     }
 }
 
-// --------------------------------------------------------------------------
-// f32: QK^T and PV on v_mfma_f32_32x32x2_f32 (full f32 products).
-// The head-dim order of the QK^T K slots is permuted (d = 8k + 4u + r) so a
-// lane reads 4 consecutive floats for 4 steps; V stays key-major in LDS.
-template <int D, int BN>
-__global__ __launch_bounds__(kAttnWaves * 64) void attn_f32_kernel(AttnArgs a) {
-  constexpr int NT = kAttnWaves * 64;
-  constexpr int KS = D + 4;
-  constexpr int NKT = BN / 32;
-  constexpr int NDT = D / 32;
-  constexpr int NQ4 = D / 8;
-  __shared__ __align__(16) float sK[BN * KS];
-  __shared__ __align__(16) float sV[BN * KS];
+// Combines the parts of split tiles: for each (row, head),
+//   M = max_s m_s,  L = sum_s 2^(m_s - M) l_s,  O = sum_s 2^(m_s - M) O_s / L.
+// One wave per (row, head), kMergeWaves per workgroup; lanes first reduce
+// the parts' (m, l) across the wave, then each lane accumulates its
+// head-dim slice over the parts with independent loads.
+constexpr int kMergeWaves = 4;
 
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int EPL = D / 64;  // head-dim values per lane
+  __shared__ float wsh[kMergeWaves][kSplitMax];
   if (!plan_ok(a)) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = lane & 31, u = lane >> 5;
-  const int kvh = blockIdx.x % a.hkv;
-  const int tile = blockIdx.x / a.hkv;
   const cev_plan_header* ph = (const cev_plan_header*)a.plan;
-  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[tile];
-  const int4* segs = (const int4*)(a.plan + ph->segs_off);
-  const int4* rows = (const int4*)(a.plan + ph->rows_off);
-  const int gi = wave % a.g, rg = wave / a.g;
-  const int head = kvh * a.g + gi;
-  const int rit = rg * 32 + n;
-  const bool row_ok = rit < td.y && td.x + rit < a.t;
-  const int row = row_ok ? td.x + rit : 0;
-
-  f32x4 qf[NQ4];
-  {
-    const float* qp = (const float*)a.q + (int64_t)row * a.q_st + (int64_t)head * a.q_sh;
-#pragma unroll
-    for (int k = 0; k < NQ4; ++k) qf[k] = row_ok ? *(const f32x4*)(qp + 8 * k + 4 * u) : f32x4{};
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // blockIdx -> (tile, row group of kMergeWaves rows, head)
+  const int tile_rows = ph->tile_rows;
+  const int groups = (tile_rows + kMergeWaves - 1) / kMergeWaves;
+  const int head = blockIdx.x % a.hq;
+  const int grp = (blockIdx.x / a.hq) % groups;
+  const int tile = blockIdx.x / (a.hq * groups);
+  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[2 * tile];
+  const int r = grp * kMergeWaves + wave;
+  if (r >= td.y || td.x + r >= a.t) return;
+  const int row = td.x + r;
+  const int64_t pf = cev_attn_partial_floats(D);
+  const int S = a.n_splits;
+  const float* rec = a.ws + ((int64_t)row * a.hq + head) * S * pf;
+  float M = -INFINITY;
+  for (int s = lane; s < S; s += 64) M = fmaxf(M, rec[s * pf + D]);
+  M = wave_max(M);
+  float L = 0.0f;
+  for (int s = lane; s < S; s += 64) {
+    const float w = fast_exp2(rec[s * pf + D] - M);
+    wsh[wave][s] = w;
+    L += w * rec[s * pf + D + 1];
   }
-  int4 rv = rows[row];
-  if (!row_ok) rv = make_int4(0, 0, -1, 0);
-
-  f32x16 o[NDT];
+  L = wave_sum(L);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  float acc[EPL];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.0f;
-
-  for (int si = 0; si < td.w; ++si) {
-    const int4 sg = clamp_seg(segs[td.z + si], a.s_cache, a.t);
-    const bool cached = sg.x < a.s_cache;
-    const float* kb = cached ? (const float*)a.kc + kvh * a.kc_sh + (int64_t)sg.x * a.kc_ss
-                             : (const float*)a.kn + kvh * a.kn_sh + (int64_t)(sg.x - a.s_cache) * a.kn_st;
-    const float* vb = cached ? (const float*)a.vc + kvh * a.vc_sh + (int64_t)sg.x * a.vc_ss
-                             : (const float*)a.vn + kvh * a.vn_sh + (int64_t)(sg.x - a.s_cache) * a.vn_st;
-    const int64_t ks = cached ? a.kc_ss : a.kn_st;
-    const int64_t vs = cached ? a.vc_ss : a.vn_st;
-    const int seg_len = sg.y - sg.x;
-    for (int k0 = 0; k0 < seg_len; k0 += BN) {
-      const int nvalid = min(BN, seg_len - k0);
-      __syncthreads();
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.0f;
+  const float* base = rec + lane * EPL;
+#pragma unroll 4
+  for (int s = 0; s < S; ++s) {
+    const float w = wsh[wave][s];
+    float v[EPL];
+    if constexpr (EPL == 2) {
+      const float2 x = *(const float2*)(base + s * pf);
+      v[0] = x.x;
+      v[1] = x.y;
+    } else {
+      const f32x4 x = *(const f32x4*)(base + s * pf);
 #pragma unroll
-      for (int v = tid; v < BN * D / 4; v += NT) {
-        const int key = v / (D / 4), c = (v % (D / 4)) * 4;
-        f32x4 x = {}, y = {};
-        if (key < nvalid) {
-          x = *(const f32x4*)(kb + (int64_t)(k0 + key) * ks + c);
-          y = *(const f32x4*)(vb + (int64_t)(k0 + key) * vs + c);
-        }
-        *(f32x4*)&sK[key * KS + c] = x;
-        *(f32x4*)&sV[key * KS + c] = y;
-      }
-      __syncthreads();
-
-      f32x16 s[NKT];
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt) {
-        s[kt] = f32x16{};
-#pragma unroll
-        for (int k = 0; k < NQ4; ++k) {
-          const f32x4 af = *(const f32x4*)&sK[(kt * 32 + n) * KS + 8 * k + 4 * u];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[r], qf[k][r], s[kt], 0, 0, 0);
-        }
-      }
-      const bool need_mask = sg.z != 0 || nvalid < BN;
-      const int key0 = sg.x + k0;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float x = s[kt][i] * a.scale_log2;
-          if (need_mask) {
-            const int kk = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
-            const int key = key0 + kk;
-            const bool vis = (kk < nvalid) & ((sg.z == 0) | ((key >= rv.x) & (key < rv.y)) | (key == rv.z));
-            x = vis ? x : -INFINITY;
-          }
-          s[kt][i] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = fmaxf(mx, swap_half(mx));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
-      float rs = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float p = fast_exp2(s[kt][i] - m_use);
-          s[kt][i] = p;
-          rs += p;
-        }
-      l_run += rs;
-      // O^T += V^T . P^T, one K=2 step per S^T register: K slot u is key
-      // 8(i/4) + 4u + i%4 of the sub-tile.
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt)
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(sV[key * KS + dt * 32 + n], s[kt][i], o[dt], 0, 0, 0);
-        }
+      for (int e = 0; e < EPL; ++e) v[e] = x[e];
     }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] += w * v[e];
   }
-
-  const float l = l_run + swap_half(l_run);
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  if (!row_ok) return;
-  float* op = (float*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
-  const float* gp = a.has_gate ? (const float*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh : nullptr;
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh + lane * EPL;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh + lane * EPL : nullptr;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = dt * 32 + 8 * q4 + 4 * u;
-      f32x4 r;
-      f32x4 gv = {};
-      if (gp) gv = *(const f32x4*)(gp + d);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float x = o[dt][4 * q4 + e] / l;
-        if (!(l > 0.0f)) x = 0.0f;
-        if (gp) x = gate_value(x, gv[e], false);
-        r[e] = x;
-      }
-      *(f32x4*)(op + d) = r;
-    }
-  (void)inv;
+  for (int e = 0; e < EPL; ++e) {
+    float x = BF ? acc[e] * inv : (L > 0.0f ? acc[e] / L : 0.0f);
+    if (gp) x = gate_value(x, (float)gp[e], BF);
+    op[e] = (T)x;
+  }
 }
 
-template <typename Kernel>
-int32_t launch(Kernel k, const AttnArgs& a, hipStream_t stream) {
-  const int64_t grid = (int64_t)a.n_tiles * a.hkv;
+template <typename T, int D>
+int32_t launch(const AttnArgs& a, hipStream_t stream) {
+  const int64_t grid = (int64_t)a.n_tiles * a.n_splits * a.hkv;
   if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "grid of %lld workgroups is too large", (long long)grid);
-  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
+  hipLaunchKernelGGL((attn_kernel<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "packed attention launch: %s", hipGetErrorString(e));
+  if (a.n_splits > 1) {
+    const int groups = (a.tile_rows + kMergeWaves - 1) / kMergeWaves;
+    const int64_t mgrid = (int64_t)a.n_tiles * groups * a.hq;
+    if (mgrid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "merge grid too large");
+    hipLaunchKernelGGL((attn_merge_kernel<T, D>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "attention merge launch: %s", hipGetErrorString(e));
+  }
   return CEV_OK;
 }
 
@@ -498,7 +548,7 @@ int32_t launch(Kernel k, const AttnArgs& a, hipStream_t stream) {
 
 extern "C" int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q,
                                         const void* k_cache, const void* v_cache, const void* k_new, const void* v_new, const void* gate,
-                                        void* out, cev_stream stream) {
+                                        void* out, void* workspace, size_t workspace_bytes, cev_stream stream) {
   CEV_CHECK_ARG(d != nullptr, "cev_packed_attention: null descriptor");
   CEV_CHECK_ARG(plan_host != nullptr && plan_dev != nullptr, "cev_packed_attention: null plan");
   const cev_plan_header* h = (const cev_plan_header*)plan_host;
@@ -511,10 +561,18 @@ extern "C" int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan
   CEV_CHECK_ARG(d->s_cache == 0 || (k_cache && v_cache), "cev_packed_attention: null cache with s_cache %d", d->s_cache);
   CEV_CHECK_ARG(!d->has_gate || gate, "cev_packed_attention: has_gate without a gate");
   const int g = d->n_q_heads / d->n_kv_heads;
-  CEV_CHECK_ARG(h->tile_rows == cev_attn_tile_rows(g), "cev_packed_attention: plan tile size mismatch");
+  CEV_CHECK_ARG(h->tile_rows == cev_attn_tile_rows(g) && h->block_n == cev_attn_block_n(d->dtype, d->head_dim) && h->n_splits >= 1,
+                "cev_packed_attention: plan tiling does not match this library");
+  size_t need = 0;
+  int32_t rc = cev_attn_workspace_size(plan_host, &need);
+  if (rc) return rc;
+  if (need > 0) {
+    CEV_CHECK_ARG(workspace != nullptr, "cev_packed_attention: the plan splits tiles and needs a %zu-byte workspace", need);
+    if (workspace_bytes < need) return cev_fail(CEV_ERR_SPACE, "workspace of %zu bytes, plan needs %zu", workspace_bytes, need);
+  }
   const uintptr_t al = 15;
   CEV_CHECK_ARG((((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)k_new | (uintptr_t)v_new | (uintptr_t)out |
-                  (uintptr_t)gate | (uintptr_t)plan_dev) & al) == 0,
+                  (uintptr_t)gate | (uintptr_t)plan_dev | (uintptr_t)workspace) & al) == 0,
                 "cev_packed_attention: device buffers must be 16-byte aligned");
   AttnArgs a;
   a.q = q;
@@ -524,6 +582,7 @@ extern "C" int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan
   a.vn = v_new;
   a.gate = gate;
   a.out = out;
+  a.ws = (float*)workspace;
   a.plan = (const int32_t*)plan_dev;
   a.q_st = d->q_stride_t;
   a.q_sh = d->q_stride_h;
@@ -542,14 +601,17 @@ extern "C" int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan
   a.n_tiles = h->n_tiles;
   a.t = d->t;
   a.s_cache = d->s_cache;
+  a.hq = d->n_q_heads;
   a.hkv = d->n_kv_heads;
   a.g = g;
   a.has_gate = d->has_gate;
+  a.n_splits = h->n_splits;
+  a.tile_rows = h->tile_rows;
   a.scale_log2 = d->scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   if (d->dtype == CEV_BF16) {
-    if (d->head_dim == 128) return launch(attn_bf16_kernel<128, 64>, a, s);
-    return launch(attn_bf16_kernel<256, 32>, a, s);
+    if (d->head_dim == 128) return launch<__bf16, 128>(a, s);
+    return launch<__bf16, 256>(a, s);
   }
-  return launch(attn_f32_kernel<128, 32>, a, s);
+  return launch<float, 128>(a, s);
 }

@@ -103,14 +103,14 @@ def test_launch_validates_before_any_gpu_call(cev):
     L = _abi.lib()
     fake = C.c_void_p(4096)
     # null plan / null buffers / a plan for other shapes: all fail before a launch
-    assert L.cev_packed_attention(C.byref(d), None, None, fake, fake, fake, fake, fake, None, fake, None) == CEV_ERR_INVALID
+    assert L.cev_packed_attention(C.byref(d), None, None, fake, fake, fake, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
     hp = C.c_void_p(plan.host.ctypes.data)
-    assert L.cev_packed_attention(C.byref(d), hp, fake, None, fake, fake, fake, fake, None, fake, None) == CEV_ERR_INVALID
+    assert L.cev_packed_attention(C.byref(d), hp, fake, None, fake, fake, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
     d2 = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 9, 10)
-    assert L.cev_packed_attention(C.byref(d2), hp, fake, fake, fake, fake, fake, fake, None, fake, None) == CEV_ERR_INVALID
-    assert L.cev_packed_attention(C.byref(d), hp, fake, fake, None, None, fake, fake, None, fake, None) == CEV_ERR_INVALID
+    assert L.cev_packed_attention(C.byref(d2), hp, fake, fake, fake, fake, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
+    assert L.cev_packed_attention(C.byref(d), hp, fake, fake, None, None, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
     d.has_gate = 1
-    assert L.cev_packed_attention(C.byref(d), hp, fake, fake, fake, fake, fake, fake, None, fake, None) == CEV_ERR_INVALID
+    assert L.cev_packed_attention(C.byref(d), hp, fake, fake, fake, fake, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
 
 
 def test_empty_table_needs_no_launch(cev):
@@ -118,7 +118,7 @@ def test_empty_table_needs_no_launch(cev):
     plan = cev_hip.AttnPlan(d, cev_hip.BlockTable([], 8, 10))
     assert plan.n_tiles == 0
     hp = C.c_void_p(plan.host.ctypes.data)
-    assert _abi.lib().cev_packed_attention(C.byref(d), hp, hp, None, None, None, None, None, None, None, None) == 0
+    assert _abi.lib().cev_packed_attention(C.byref(d), hp, hp, None, None, None, None, None, None, None, None, 0, None) == 0
 
 
 def test_qknorm_validation(cev):
@@ -217,9 +217,10 @@ def test_plan_tiles_cover_rows_and_keys(cev, orc):
             d = cev_hip.attn_desc(CEV_BF16, hq, hkv, 128, tab.t, tab.s_cache)
             plan = cev_hip.AttnPlan(d, tab)
             dense = tab.to_dense_mask() == 0
-            rows = plan.host.view(np.int32)[plan.host[:64].view(np.int32)[13]:].reshape(-1, 4)[: tab.t]
+            rows = plan.rows()
             seen = np.zeros_like(dense)
-            for tr0, tn, s0, sn in plan.tiles():
+            for tr0, tn, s0, sn, nch, _, _, _ in plan.tiles():
+                assert nch == sum(-(-(ke - kb) // plan.block_n) for kb, ke, _, _ in plan.segs()[s0:s0 + sn])
                 assert tn <= plan.tile_rows
                 for kb, ke, masked, _ in plan.segs()[s0:s0 + sn]:
                     assert (kb < tab.s_cache) == (ke <= tab.s_cache) or kb >= tab.s_cache
@@ -231,3 +232,34 @@ def test_plan_tiles_cover_rows_and_keys(cev, orc):
                         assert not seen[r, keys].any(), "a key visited twice"
                         seen[r, keys] = True
             assert np.array_equal(seen, dense)
+
+
+def test_split_policy(cev):
+    """Few long-prefix rows split their key stream; full grids do not."""
+    B = cev_hip.BlockTable.block
+    hbm = cev_hip.BlockTable([B(0, 16, 32768, spans=[(0, 32768)])], 16, 32768)
+    d = cev_hip.attn_desc(CEV_BF16, 32, 8, 128, 16, 32768)
+    p = cev_hip.AttnPlan(d, hbm)
+    assert p.n_splits > 1 and p.n_tiles * p.n_splits * 8 >= 512
+    assert p.workspace_bytes == 16 * 32 * p.n_splits * (128 + 4) * 4
+    d.max_splits = 1
+    assert cev_hip.AttnPlan(d, hbm).n_splits == 1 and cev_hip.AttnPlan(d, hbm).workspace_bytes == 0
+    d.max_splits = 3
+    assert cev_hip.AttnPlan(d, hbm).n_splits == 3
+    plans, items = [(32768, 32768, 32768)], [(0, 64)] * 64
+    tab, _, _ = cev_hip.BlockTable.from_plans(plans, items)
+    d = cev_hip.attn_desc(CEV_BF16, 32, 8, 128, tab.t, tab.s_cache)
+    assert cev_hip.AttnPlan(d, tab).n_splits == 1
+
+
+def test_launch_requires_workspace_for_split_plans(cev):
+    B = cev_hip.BlockTable.block
+    tab = cev_hip.BlockTable([B(0, 16, 4096, spans=[(0, 4096)])], 16, 4096)
+    d = cev_hip.attn_desc(CEV_BF16, 32, 8, 128, 16, 4096)
+    plan = cev_hip.AttnPlan(d, tab)
+    assert plan.n_splits > 1
+    fake = C.c_void_p(4096)
+    hp = C.c_void_p(plan.host.ctypes.data)
+    L = _abi.lib()
+    assert L.cev_packed_attention(C.byref(d), hp, fake, fake, fake, fake, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
+    assert L.cev_packed_attention(C.byref(d), hp, fake, fake, fake, fake, fake, fake, None, fake, fake, 16, None) == CEV_ERR_SPACE

@@ -136,8 +136,8 @@ def test_small_packed_passes(gpu, orc, case):
 
 def test_packed_equals_each_block_alone_on_gpu(gpu):
     """qwen3.rs:13-17: packing is exactly asking each question alone.  The
-    kernel visits the same key tiles in the same order either way, so the
-    outputs agree bit for bit at the full c3 shape."""
+    kernel visits the same key tiles in the same order either way (unsplit),
+    so the outputs agree bit for bit at the full c3 shape."""
     w = configs.c3()
     gl = GpuLayer(w, gpu)
     gl.forward()
@@ -145,7 +145,8 @@ def test_packed_equals_each_block_alone_on_gpu(gpu):
     for b in (0, 41):
         r0, L = int(w.block_starts()[b]), w.blocks[b]
         tab = cev_hip.BlockTable.from_rows(1, L, w.prefix, causal=True)
-        alone = cev_hip.packed_attention(gl.q[r0:r0 + L], gl.k[r0:r0 + L], gl.v[r0:r0 + L], tab, k_cache=gl.pk, v_cache=gl.pv)
+        alone = cev_hip.packed_attention(gl.q[r0:r0 + L], gl.k[r0:r0 + L], gl.v[r0:r0 + L], tab, k_cache=gl.pk, v_cache=gl.pv,
+                                         max_splits=1)
         assert np.array_equal(to_np(alone), packed[r0:r0 + L])
 
 
@@ -218,3 +219,41 @@ def test_kernel_repeats_bitwise(gpu):
     a = to_np(gl.out).copy()
     gl.forward()
     assert np.array_equal(a, to_np(gl.out))
+
+
+@pytest.mark.parametrize("blocks", [1, 4])
+def test_long_prefix_short_suffix_split(gpu, orc, blocks):
+    """The HBM-bound shape: c3's 32768-key prefix with 16-token blocks.  The
+    planner splits each tile's key stream; the merged result matches the
+    oracle and the unsplit kernel."""
+    w = configs.hbm(blocks)
+    _say(f"test {w.name}: t={w.t} P={w.prefix}")
+    gl = GpuLayer(w, gpu)
+    assert gl.attn.plan.n_splits > 1
+    ol = OracleLayer(orc, w, gl.np_inputs)
+    gl.forward()
+    _check_blocks(gl, ol, range(len(w.blocks)), BF16_TOL)
+    split = to_np(gl.out).copy()
+    whole = cev_hip.packed_attention(gl.q, gl.k, gl.v, gl.table, k_cache=gl.pk, v_cache=gl.pv, max_splits=1)
+    assert np.abs(to_np(whole) - split).max() <= 4e-3
+
+
+def test_split_f32_matches_unsplit(gpu):
+    w = configs.c1()
+    gl = GpuLayer(w, gpu)
+    gl.forward()
+    assert gl.attn.plan.n_splits > 1
+    split = to_np(gl.out).copy()
+    whole = cev_hip.packed_attention(gl.q, gl.k, gl.v, gl.table, k_cache=gl.pk, v_cache=gl.pv, max_splits=1)
+    assert np.abs(to_np(whole) - split).max() <= 1e-6
+
+
+def test_split_gated_rows(gpu, orc):
+    """Gate epilogue in the merge pass (c5a splits its 128 workgroups)."""
+    w = configs.c5_attention()
+    tab = cev_hip.BlockTable.from_rows(len(w.blocks), w.blocks[0], w.prefix, causal=True)
+    gl = GpuLayer(w, gpu, table=tab)
+    assert gl.attn.plan.n_splits > 1
+    ol = OracleLayer(orc, w, gl.np_inputs)
+    gl.forward()
+    _check_blocks(gl, ol, [3, 17], BF16_TOL)
