@@ -105,6 +105,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c3", choices=["c1", "c3", "c4", "c5a", "hbm"])
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline leg")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of the workload, run `steps` device copies of MIB MiB (the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -118,6 +121,15 @@ def main():
     from cev_hip.layer import AttentionLayer
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n, "launches": args.warmup + args.steps}), flush=True)
+        return
     w = configs.WORKLOADS[args.workload]()
     layer = AttentionLayer(w, dev)
     for _ in range(args.warmup):

@@ -9,7 +9,7 @@ import ctypes as C
 import os
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG, "build", "libcev_hip.so")
+LIB_PATH = os.environ.get("CEV_HIP_LIB") or os.path.join(_PKG, "build", "libcev_hip.so")
 
 CEV_OK = 0
 CEV_ERR_INVALID = -1

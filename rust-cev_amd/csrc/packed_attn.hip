@@ -103,10 +103,15 @@ __device__ __forceinline__ bf16x4 lds_read_tr(const __bf16* p) {
 template <typename T, int D>
 struct Frag;
 
+#ifndef CEV_VPAD_BF16
+#define CEV_VPAD_BF16 32
+#endif
+
 template <int D>
 struct Frag<__bf16, D> {
   static constexpr int BN = D == 128 ? 64 : 32;
   static constexpr int PAD = 8;
+  static constexpr int VPAD = CEV_VPAD_BF16;
   static constexpr int VEC = 8;
   typedef bf16x8 Vec;
   bf16x8 q[D / 16];
@@ -160,6 +165,7 @@ template <int D>
 struct Frag<float, D> {
   static constexpr int BN = 32;
   static constexpr int PAD = 4;
+  static constexpr int VPAD = 4;
   static constexpr int VEC = 4;
   typedef f32x4 Vec;
   f32x4 q[D / 8];
@@ -226,14 +232,15 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
   constexpr int BN = F::BN;
   constexpr int NT = kAttnWaves * 64;
   constexpr int VEC = F::VEC;
-  constexpr int RS = D + F::PAD;  // LDS row stride (elements) of K and V tiles
-  constexpr int TILE = BN * RS;   // one K or V tile
+  constexpr int RS = D + F::PAD;    // LDS row stride (elements) of the K tile
+  constexpr int RSV = D + F::VPAD;  // LDS row stride of the V tile
+  constexpr int TILE = BN * RS + BN * RSV;  // one K tile then one V tile
   constexpr int NKT = BN / 32;    // 32-key sub-tiles per key tile
   constexpr int NDT = D / 32;     // 32-wide slices of the head dim
   constexpr int NLD = BN * D / VEC / NT;  // 16-byte loads per thread per tensor
   static_assert(BN * D / VEC % NT == 0, "tile loads must split evenly");
   typedef typename F::Vec Vec;
-  __shared__ __align__(16) T smem[2 * 2 * TILE];
+  __shared__ __align__(16) T smem[2 * TILE];
 
   if (!plan_ok(a)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -323,13 +330,14 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
     }
   };
   auto store = [&](int buf) {
-    T* sk = smem + buf * 2 * TILE;
+    T* sk = smem + buf * TILE;
+    T* sv = sk + BN * RS;
 #pragma unroll
     for (int r = 0; r < NLD; ++r) {
       const int v = tid + r * NT;
       const int key = v / (D / VEC), col = (v % (D / VEC)) * VEC;
       *(Vec*)&sk[key * RS + col] = kreg[r];
-      *(Vec*)&sk[TILE + key * RS + col] = vreg[r];
+      *(Vec*)&sv[key * RSV + col] = vreg[r];
     }
   };
 
@@ -345,8 +353,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
       const bool more = ci + 1 < my_chunks && nsi < nseg;
       if (more) load(nsi, nk0);  // in flight while this tile is scored
 
-      const T* sK = smem + buf * 2 * TILE;
-      const T* sV = sK + TILE;
+      const T* sK = smem + buf * TILE;
+      const T* sV = sK + BN * RS;
       const int4 sg = seg_of(si);
       const int key0 = sg.x + k0;
       const int nvalid = min(BN, sg.y - key0);
@@ -396,7 +404,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
         }
       l_run += rs;
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt) fr.template pv<RS>(sV, kt, lane, u, s[kt], o);
+      for (int kt = 0; kt < NKT; ++kt) fr.template pv<RSV>(sV, kt, lane, u, s[kt], o);
       }
 
       if (!more) break;
