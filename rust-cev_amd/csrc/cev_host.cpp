@@ -155,6 +155,19 @@ int32_t check_desc(const cev_attn_desc* d) {
   const int64_t al = d->dtype == CEV_BF16 ? 8 : 4;
   for (const int64_t* s : st)
     if (*s % al) return cev_fail(CEV_ERR_UNSUPPORTED, "strides must be multiples of %lld elements", (long long)al);
+  // K/V tiles are fetched with buffer loads whose byte range ends at the
+  // tile's last valid key: rows must not overlap, and a tile of keys must
+  // span less than 2 GiB.
+  const int64_t esz = d->dtype == CEV_BF16 ? 2 : 4;
+  const int64_t span_max = (INT32_MAX / 2) / 64 / esz;
+  const int64_t* rows_c[] = {&d->kc_stride_s, &d->vc_stride_s};
+  const int64_t* rows_n[] = {&d->kn_stride_t, &d->vn_stride_t};
+  for (const int64_t* s : rows_c)
+    if (d->s_cache > 0 && (*s < d->head_dim || *s > span_max))
+      return cev_fail(CEV_ERR_UNSUPPORTED, "cache row stride %lld outside [head_dim, %lld]", (long long)*s, (long long)span_max);
+  for (const int64_t* s : rows_n)
+    if (d->t > 0 && (*s < d->head_dim || *s > span_max))
+      return cev_fail(CEV_ERR_UNSUPPORTED, "new K/V row stride %lld outside [head_dim, %lld]", (long long)*s, (long long)span_max);
   if (d->has_gate) {
     CEV_CHECK_ARG(d->g_stride_t >= 0 && d->g_stride_h >= 0, "negative gate stride");
     if (d->g_stride_t % al || d->g_stride_h % al) return cev_fail(CEV_ERR_UNSUPPORTED, "gate strides must be multiples of %lld", (long long)al);

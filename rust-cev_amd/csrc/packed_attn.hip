@@ -23,6 +23,8 @@
 //     KV head and its K/V stream stays in that XCD's L2;
 //   - a split tile writes (unnormalised O, m, l) per row and head to the
 //     workspace and attn_merge_kernel combines the parts.
+#include <type_traits>
+
 #include "cev_device.h"
 #include "cev_internal.h"
 #include "cev_plan.h"
@@ -100,6 +102,12 @@ __device__ __forceinline__ bf16x4 lds_read_tr(const __bf16* p) {
 // f32 (v_mfma_f32_32x32x2_f32, full f32 products): the head-dim order of
 // the QK^T K slots is permuted (d = 8k + 4u + r) so a lane reads 4
 // consecutive floats for 4 steps; one K=2 PV step per S^T register.
+//
+// Both expose the work as small steps so the main loop can interleave the
+// MFMAs of one sub-tile with the VALU work of another:
+//   qk_step(st), st < NQK   - builds one 32x32 S^T sub-tile;
+//   pv_step(j),  j < NPV    - adds one sub-tile's V^T . P^T to O;
+//   make_p                  - probabilities -> PV operand, plus their sum.
 template <typename T, int D>
 struct Frag;
 
@@ -107,13 +115,20 @@ struct Frag;
 #define CEV_VPAD_BF16 32
 #endif
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 template <int D>
 struct Frag<__bf16, D> {
   static constexpr int BN = D == 128 ? 64 : 32;
   static constexpr int PAD = 8;
   static constexpr int VPAD = CEV_VPAD_BF16;
   static constexpr int VEC = 8;
+  static constexpr int NQK = D / 16;
+  static constexpr int NPV = 2 * (D / 32);
   typedef bf16x8 Vec;
+  struct P {
+    bf16x8 h[2];
+  };
   bf16x8 q[D / 16];
 
   __device__ __forceinline__ void load_q(const __bf16* qp, bool ok, int u) {
@@ -124,40 +139,54 @@ struct Frag<__bf16, D> {
     }
   }
 
+  // K operand of QK step st: key kt*32 + n, head-dim values 16st + 8u ..
   template <int RS>
-  __device__ __forceinline__ f32x16 qk(const __bf16* sK, int kt, int n, int u) const {
-    f32x16 s = {};
-#pragma unroll
-    for (int st = 0; st < D / 16; ++st) {
-      const bf16x8 af = *(const bf16x8*)&sK[(kt * 32 + n) * RS + 16 * st + 8 * u];
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, q[st], s, 0, 0, 0);
-    }
-    return s;
+  __device__ __forceinline__ static bf16x8 k_frag(const __bf16* sK, int kt, int st, int n, int u) {
+    return *(const bf16x8*)&sK[(kt * 32 + n) * RS + 16 * st + 8 * u];
+  }
+  __device__ __forceinline__ void qk_mfma(const bf16x8& af, int st, f32x16& s) const {
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, q[st], s, 0, 0, 0);
+  }
+  template <int RS>
+  __device__ __forceinline__ void qk_step(const __bf16* sK, int kt, int st, int n, int u, f32x16& s) const {
+    qk_mfma(k_frag<RS>(sK, kt, st, n, u), st, s);
   }
 
-  // o[dt] += V^T . P^T for one 32-key sub-tile kt whose probabilities are p.
-  template <int RS>
-  __device__ __forceinline__ void pv(const __bf16* sV, int kt, int lane, int u, const f32x16& p, f32x16* o) const {
-    bf16x8 pf[2];
+  // The row sum is taken over the bf16 probabilities PV multiplies, on the
+  // dot-product unit (two products per instruction).
+  __device__ __forceinline__ static void make_p(const f32x16& e, P& p, float& rs) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pf[h][j] = (__bf16)p[8 * h + j];
-    // Lane (group g16 = lane/16, i = lane%16) reads row kb + i/4, columns
-    // d0 + 4(i%4) .. +3; the transpose load hands it 4 consecutive keys of
-    // head-dim column d0 + i.
+      for (int j = 0; j < 8; ++j) p.h[h][j] = (__bf16)e[8 * h + j];
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) rs = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p.h[h][j], p.h[h][j + 1]}, one, rs, false);
+  }
+
+  // Step j = h * (D/32) + dt: o[dt] += V^T(keys of half h) . P^T(half h).
+  // Lane (group g16 = lane/16, i = lane%16) reads row kb + i/4, columns
+  // d0 + 4(i%4) .. +3; the transpose load hands it 4 consecutive keys of
+  // head-dim column d0 + i.
+  template <int RS>
+  __device__ __forceinline__ static bf16x8 v_frag(const __bf16* sV, int kt, int j, int lane, int u) {
+    const int h = j / (D / 32), dt = j % (D / 32);
     const int tr_row = (lane & 15) >> 2;
     const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        const __bf16* vp = sV + (kt * 32 + 16 * h + 4 * u + tr_row) * RS + dt * 32 + tr_col;
-        const bf16x4 lo = lds_read_tr(vp);
-        const bf16x4 hi = lds_read_tr(vp + 8 * RS);
-        const bf16x8 af = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, pf[h], o[dt], 0, 0, 0);
-      }
+    const __bf16* vp = sV + (kt * 32 + 16 * h + 4 * u + tr_row) * RS + dt * 32 + tr_col;
+    const bf16x4 lo = lds_read_tr(vp);
+    const bf16x4 hi = lds_read_tr(vp + 8 * RS);
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  __device__ __forceinline__ static void pv_mfma(const bf16x8& af, int j, const P& p, f32x16* o) {
+    const int h = j / (D / 32), dt = j % (D / 32);
+    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, p.h[h], o[dt], 0, 0, 0);
+  }
+  template <int RS>
+  __device__ __forceinline__ void pv_step(const __bf16* sV, int kt, int j, int lane, int u, const P& p, f32x16* o) const {
+    pv_mfma(v_frag<RS>(sV, kt, j, lane, u), j, p, o);
   }
 };
 
@@ -167,7 +196,12 @@ struct Frag<float, D> {
   static constexpr int PAD = 4;
   static constexpr int VPAD = 4;
   static constexpr int VEC = 4;
+  static constexpr int NQK = D / 8;
+  static constexpr int NPV = 16;
   typedef f32x4 Vec;
+  struct P {
+    f32x16 v;
+  };
   f32x4 q[D / 8];
 
   __device__ __forceinline__ void load_q(const float* qp, bool ok, int u) {
@@ -176,26 +210,24 @@ struct Frag<float, D> {
   }
 
   template <int RS>
-  __device__ __forceinline__ f32x16 qk(const float* sK, int kt, int n, int u) const {
-    f32x16 s = {};
+  __device__ __forceinline__ void qk_step(const float* sK, int kt, int k, int n, int u, f32x16& s) const {
+    const f32x4 af = *(const f32x4*)&sK[(kt * 32 + n) * RS + 8 * k + 4 * u];
 #pragma unroll
-    for (int k = 0; k < D / 8; ++k) {
-      const f32x4 af = *(const f32x4*)&sK[(kt * 32 + n) * RS + 8 * k + 4 * u];
+    for (int r = 0; r < 4; ++r) s = __builtin_amdgcn_mfma_f32_32x32x2f32(af[r], q[k][r], s, 0, 0, 0);
+  }
+
+  __device__ __forceinline__ static void make_p(const f32x16& e, P& p, float& rs) {
+    p.v = e;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s = __builtin_amdgcn_mfma_f32_32x32x2f32(af[r], q[k][r], s, 0, 0, 0);
-    }
-    return s;
+    for (int i = 0; i < 16; ++i) rs += e[i];
   }
 
   template <int RS>
-  __device__ __forceinline__ void pv(const float* sV, int kt, int lane, int u, const f32x16& p, f32x16* o) const {
+  __device__ __forceinline__ void pv_step(const float* sV, int kt, int i, int lane, int u, const P& p, f32x16* o) const {
     const int n = lane & 31;
+    const int key = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(sV[key * RS + dt * 32 + n], p[i], o[dt], 0, 0, 0);
-    }
+    for (int dt = 0; dt < D / 32; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(sV[key * RS + dt * 32 + n], p.v[i], o[dt], 0, 0, 0);
   }
 };
 
@@ -224,9 +256,430 @@ __device__ __forceinline__ void load_vec4<float>(const float* p, float* v) {
   for (int e = 0; e < 4; ++e) v[e] = g[e];
 }
 
+// Word 3 of a raw buffer resource on gfx9: 32-bit data format, no swizzle.
+constexpr int kBufferWord3 = 0x00020000;
+
+// Values the compiler cannot prove wave-uniform (they come through vector
+// loads of the plan) but are: readfirstlane moves them to SGPRs, where a
+// buffer resource must live.
+__device__ __forceinline__ int uniform_i32(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Keeps a value computed where it stands: sched_barrier only fences the
+// machine scheduler, and without a use the IR passes sink the row max and
+// row sum past the MFMAs they are meant to overlap.
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+
+// One BN-key chunk of a tile's key stream: keys key0 .. key0 + BN, the first
+// nvalid of them inside the segment; local != 0 when the segment's keys are
+// masked per row.
+struct Chunk {
+  int key0, nvalid, local;
+};
+
+// Cursor over the BN-key chunks of a tile's segments.  The current segment,
+// clamped, stays in SGPRs; the plan is read only when the cursor enters a
+// new segment (readfirstlane tells the compiler these vector-loaded values
+// are wave-uniform).
+template <int BN>
+struct ChunkCursor {
+  const int4* segs;
+  int nseg, s_cache, t;
+  int si, k0;
+  int4 cur;
+
+  __device__ __forceinline__ int4 seg(int i) const {
+    const int4 sg = clamp_seg(segs[i], s_cache, t);
+    return make_int4(uniform_i32(sg.x), uniform_i32(sg.y), uniform_i32(sg.z), 0);
+  }
+  // Positions the cursor on chunk c of the tile's stream.
+  __device__ __forceinline__ void seek(int c) {
+    si = 0;
+    k0 = 0;
+    cur = make_int4(0, 0, 0, 0);
+    for (; si < nseg; ++si) {
+      cur = seg(si);
+      const int nch = (max(0, cur.y - cur.x) + BN - 1) / BN;
+      if (c < nch) {
+        k0 = c * BN;
+        return;
+      }
+      c -= nch;
+    }
+  }
+  __device__ __forceinline__ bool valid() const { return si < nseg; }
+  __device__ __forceinline__ void next() {
+    k0 += BN;
+    if (cur.x + k0 < cur.y) return;
+    k0 = 0;
+    for (++si; si < nseg; ++si) {
+      cur = seg(si);
+      if (cur.y > cur.x) return;
+    }
+  }
+  __device__ __forceinline__ Chunk here() const {
+    Chunk ch{0, 0, 0};
+    if (si < nseg) {
+      ch.key0 = cur.x + k0;
+      ch.nvalid = max(0, min(BN, cur.y - ch.key0));
+      ch.local = cur.z;
+    }
+    return ch;
+  }
+};
+
+// K/V rows of one KV head (cache rows [0, s_cache), then the new rows),
+// fetched with buffer loads whose byte range ends at a chunk's last valid
+// key: rows past it read as zero.
+template <typename T>
+struct KvSource {
+  uint64_t kc, vc, kn, vn;         // row 0 of this head
+  int kc_rb, vc_rb, kn_rb, vn_rb;  // row strides in bytes
+  int s_cache;
+
+  __device__ __forceinline__ void init(const AttnArgs& a, int kvh) {
+    kc = (uint64_t)((const T*)a.kc + kvh * a.kc_sh);
+    vc = (uint64_t)((const T*)a.vc + kvh * a.vc_sh);
+    kn = (uint64_t)((const T*)a.kn + kvh * a.kn_sh);
+    vn = (uint64_t)((const T*)a.vn + kvh * a.vn_sh);
+    kc_rb = (int)(a.kc_ss * (int64_t)sizeof(T));
+    vc_rb = (int)(a.vc_ss * (int64_t)sizeof(T));
+    kn_rb = (int)(a.kn_st * (int64_t)sizeof(T));
+    vn_rb = (int)(a.vn_st * (int64_t)sizeof(T));
+    s_cache = a.s_cache;
+  }
+  // Buffer resources for chunk ch and the row strides they use.
+  __device__ __forceinline__ void rsrc(const Chunk& ch, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv, int& kr, int& vr) const {
+    const bool cached = ch.key0 < s_cache;
+    kr = uniform_i32(cached ? kc_rb : kn_rb);
+    vr = uniform_i32(cached ? vc_rb : vn_rb);
+    const int64_t row0 = cached ? ch.key0 : ch.key0 - s_cache;
+    const uint64_t kp = uniform_u64((cached ? kc : kn) + (uint64_t)(row0 * kr));
+    const uint64_t vp = uniform_u64((cached ? vc : vn) + (uint64_t)(row0 * vr));
+    rk = __builtin_amdgcn_make_buffer_rsrc((void*)kp, (short)0, uniform_i32(ch.nvalid * kr), kBufferWord3);
+    rv = __builtin_amdgcn_make_buffer_rsrc((void*)vp, (short)0, uniform_i32(ch.nvalid * vr), kBufferWord3);
+  }
+};
+
+// Loads this thread's share of chunk ch (NLD 16-byte vectors per tensor).
+template <typename T, int D, int NLD, int NT, typename Vec>
+__device__ __forceinline__ void load_chunk(const KvSource<T>& src, const Chunk& ch, int tid, Vec* kreg, Vec* vreg) {
+  constexpr int VEC = 16 / sizeof(T);
+  __amdgpu_buffer_rsrc_t rk, rv;
+  int kr, vr;
+  src.rsrc(ch, rk, rv, kr, vr);
+#pragma unroll
+  for (int r = 0; r < NLD; ++r) {
+    const int v = tid + r * NT;
+    const int key = v / (D / VEC), col = (v % (D / VEC)) * VEC;
+    kreg[r] = __builtin_bit_cast(Vec, __builtin_amdgcn_raw_buffer_load_b128(rk, key * kr + col * (int)sizeof(T), 0, 0));
+    vreg[r] = __builtin_bit_cast(Vec, __builtin_amdgcn_raw_buffer_load_b128(rv, key * vr + col * (int)sizeof(T), 0, 0));
+  }
+}
+
 // --------------------------------------------------------------------------
+// bf16, d = 128: the MFMA and VALU halves of consecutive 32-key sub-tiles
+// overlap inside each wave (the loop below says how).  Two waves share a
+// SIMD at 256 VGPRs, and the per-chunk barrier keeps them in step, so a
+// wave cannot rely on the other one to fill its idle issue slots.
 template <typename T, int D>
-__global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_kernel_pipe(AttnArgs a) {
+  using F = Frag<T, D>;
+  using P = typename F::P;
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int BN = F::BN;
+  constexpr int NT = kAttnWaves * 64;
+  constexpr int VEC = F::VEC;
+  constexpr int RS = D + F::PAD;    // LDS row stride (elements) of a K tile
+  constexpr int RSV = D + F::VPAD;  // LDS row stride of a V tile
+  constexpr int KT = BN * RS;
+  constexpr int VT = BN * RSV;
+  constexpr int NKT = BN / 32;    // 32-key sub-tiles per chunk
+  constexpr int NDT = D / 32;     // 32-wide slices of the head dim
+  constexpr int NLD = BN * D / VEC / NT;  // 16-byte loads per thread per tensor
+  constexpr int EPQ = 16 / F::NQK;        // exponentials per QK step
+  constexpr int MPV = 16 / F::NPV;        // max operands per PV step
+  static_assert(BN * D / VEC % NT == 0, "tile loads must split evenly");
+  static_assert(EPQ * F::NQK == 16 && MPV * F::NPV == 16, "interleave must cover a sub-tile");
+  static_assert(BF && D == 128, "the pipelined loop is sized for bf16, d = 128");
+  typedef typename F::Vec Vec;
+  __shared__ __align__(16) T smem[3 * KT + 3 * VT];
+  T* const kbuf = smem;
+  T* const vbuf = smem + 3 * KT;
+
+  if (!plan_ok(a)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, u = lane >> 5;
+  const int kvh = blockIdx.x % a.hkv;
+  const int item = blockIdx.x / a.hkv;
+  const int tile = item / a.n_splits, part = item % a.n_splits;
+  const cev_plan_header* ph = (const cev_plan_header*)a.plan;
+  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[2 * tile];
+  const int n_chunks = ((const int4*)(a.plan + ph->tiles_off))[2 * tile + 1].x;
+  const int4* segs = (const int4*)(a.plan + ph->segs_off) + td.z;
+  const int nseg = td.w;
+  const int4* rows = (const int4*)(a.plan + ph->rows_off);
+  // Query slot (wave, n) holds row slot / g of the tile, query head slot % g:
+  // the valid rows of a short tile fill the first waves, and a wave with no
+  // valid row skips the MFMA work (it still helps stage K/V).
+  const int slot = wave * 32 + n;
+  const int gi = slot % a.g;
+  const int head = kvh * a.g + gi;
+  const int rit = slot / a.g;
+  const bool row_ok = rit < td.y && td.x + rit < a.t;
+  const int row = row_ok ? td.x + rit : 0;
+  const bool wave_active = (wave * 32) / a.g < td.y;
+  const float c = a.scale_log2;
+
+  F fr;
+  fr.load_q((const T*)a.q + (int64_t)row * a.q_st + (int64_t)head * a.q_sh, row_ok, u);
+  int4 rv = rows[row];
+  if (!row_ok) rv = make_int4(0, 0, -1, 0);
+
+  f32x16 o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
+  float m_run = -1e30f, l_run = 0.0f;
+
+  // ---- this part's slice of the tile's key stream: chunks [c0, c1)
+  const int c0 = (int)((int64_t)part * n_chunks / a.n_splits);
+  const int c1 = (int)((int64_t)(part + 1) * n_chunks / a.n_splits);
+  ChunkCursor<BN> cursor{segs, nseg, a.s_cache, a.t, 0, 0, make_int4(0, 0, 0, 0)};
+  cursor.seek(c0);
+  KvSource<T> kvs;
+  kvs.init(a, kvh);
+  Vec kreg[NLD], vreg[NLD];
+  auto load = [&](const Chunk& ch) { load_chunk<T, D, NLD, NT, Vec>(kvs, ch, tid, kreg, vreg); };
+  auto store = [&](T* sk, T* sv) {
+#pragma unroll
+    for (int r = 0; r < NLD; ++r) {
+      const int v = tid + r * NT;
+      const int key = v / (D / VEC), col = (v % (D / VEC)) * VEC;
+      *(Vec*)&sk[key * RS + col] = kreg[r];
+      *(Vec*)&sv[key * RSV + col] = vreg[r];
+    }
+  };
+  auto needs_mask = [](const Chunk& ch) { return ch.local != 0 || ch.nvalid < BN; };
+  // Masks sub-tile kt of chunk ch in place and returns its lane-local max.
+  auto mask_sub = [&](f32x16& s, int kt, const Chunk& ch) {
+    // Branch-free on purpose: a short-circuit && / || here gives every
+    // element its own control flow, and hipcc 7.2 then reuses the score
+    // register of element 0 for `key` and drops its select.
+    const bool all_rows = ch.local == 0;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kk = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
+      const int key = ch.key0 + kk;
+      const bool vis = (kk < ch.nvalid) & (all_rows | ((key >= rv.x) & (key < rv.y)) | (key == rv.z));
+      s[i] = vis ? s[i] : -INFINITY;
+      mx = fmaxf(mx, s[i]);
+    }
+    return mx;
+  };
+
+  // ---- main loop, software-pipelined over 32-key sub-tiles j:
+  //   scores S(j+1) = K(j+1) . Q^T run on the MFMA unit while the VALU turns
+  //   S(j) into probabilities; then O += V(j)^T . P(j) runs while the VALU
+  //   takes the row max of S(j+1).  The softmax max and the lazy rescale
+  //   are per sub-tile.  K and V tiles are triple-buffered in LDS: during
+  //   iteration i the waves read K of chunks i and i+1 and V of chunk i
+  //   while chunk i+2 is written into the buffers chunk i-1 used; chunk
+  //   i+3 is fetched into registers during iteration i, so one barrier per
+  //   chunk orders every LDS reuse.
+  const int nc = c1 - c0;
+  if (nc > 0 && cursor.valid()) {
+    Chunk ch1{0, 0, 0}, ch2{0, 0, 0}, ch3{0, 0, 0};  // chunks i+1, i+2, i+3
+    Chunk ch0 = cursor.here();                       // chunk i
+    load(ch0);
+    store(kbuf, vbuf);
+    if (nc > 1) {
+      cursor.next();
+      ch1 = cursor.here();
+      load(ch1);
+      store(kbuf + KT, vbuf + VT);
+    }
+    if (nc > 2) {
+      cursor.next();
+      ch2 = cursor.here();
+      load(ch2);
+    }
+    __syncthreads();
+    f32x16 sa, sb;
+    float mx = -INFINITY;  // lane-local max of the current sub-tile
+    if (wave_active) {
+      sa = f32x16{};
+#pragma unroll
+      for (int st = 0; st < F::NQK; ++st) fr.template qk_step<RS>(kbuf, 0, st, n, u, sa);
+      if (needs_mask(ch0)) {
+        mx = mask_sub(sa, 0, ch0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sa[i]);
+      }
+    }
+
+    // One chunk; on entry s_in holds S of its first sub-tile.
+    auto step = [&](int ci, f32x16& s_in, f32x16& s_other) {
+      const bool has1 = ci + 1 < nc, has2 = ci + 2 < nc, has3 = ci + 3 < nc;
+      const int b0 = ci % 3, b1 = b0 == 2 ? 0 : b0 + 1, b2 = b1 == 2 ? 0 : b1 + 1;  // buffers of chunks ci, ci+1, ci+2
+      const T* k_cur = kbuf + b0 * KT;
+      const T* k_next = kbuf + b1 * KT;
+      const T* v_cur = vbuf + b0 * VT;
+      // chunk ci+2 into the buffers chunk ci-1 used: its last reads were
+      // before the previous barrier
+      if (has2) store(kbuf + b2 * KT, vbuf + b2 * VT);
+      if (has3) {
+        cursor.next();
+        ch3 = cursor.here();
+        load(ch3);
+      }
+      if (wave_active) {
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+          f32x16& s = kt % 2 == 0 ? s_in : s_other;
+          f32x16& sn = kt % 2 == 0 ? s_other : s_in;
+          const bool last = kt + 1 == NKT;
+          const T* kn_ptr = last ? k_next : k_cur;
+          const int ktn = last ? 0 : kt + 1;
+          // lazy rescale against this sub-tile's row max
+          {
+            const float m_cand = pair_max(mx) * c;
+            const bool grow = m_cand > m_run + kRescale;
+            if (__ballot(grow)) {
+              const float m_new = grow ? m_cand : m_run;
+              const float alpha = fast_exp2(m_run - m_new);
+              m_run = m_new;
+              l_run *= alpha;
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+            }
+          }
+          const float mc = -m_run;
+          float rs = 0.0f, m2 = -INFINITY;
+          // One straight-line block per case, so the scheduler pairs the
+          // MFMAs of one stream with the VALU work of the other.
+          auto body = [&](auto has_next_tag) {
+            constexpr bool HN = decltype(has_next_tag)::value;
+            constexpr int KPF = 3;  // K fragments in flight ahead of their MFMA
+            constexpr int VPF = 3;  // V fragments in flight ahead of their MFMA
+            static_assert(EPQ == 2 && MPV == 2 && F::NQK == 8 && F::NPV == 8, "unit layout below");
+            // Each unit below ends in a scheduling fence, so the order is
+            // the program order unit by unit: one MFMA of one stream next to
+            // the VALU work of the other, with operand reads KPF / VPF units
+            // ahead of their MFMA.
+            bf16x8 kf[KPF], vf[VPF];
+            P p;
+            if constexpr (HN) {
+              sn = f32x16{};
+#pragma unroll
+              for (int f = 0; f < KPF; ++f) kf[f] = F::template k_frag<RS>(kn_ptr, ktn, f, n, u);
+            }
+            const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+            // Region A: QK(j+1) on the MFMA unit; exp(j), P(j) and its row sum
+            // on the VALU, two probabilities per unit.
+#pragma unroll
+            for (int st = 0; st < F::NQK; ++st) {
+              if constexpr (HN) {
+                fr.qk_mfma(kf[st % KPF], st, sn);
+                if (st + KPF < F::NQK) kf[st % KPF] = F::template k_frag<RS>(kn_ptr, ktn, st + KPF, n, u);
+              }
+              if (st >= F::NQK - VPF) vf[st - (F::NQK - VPF)] = F::template v_frag<RSV>(v_cur, kt, st - (F::NQK - VPF), lane, u);
+              const float e0 = fast_exp2(__builtin_fmaf(s[2 * st], c, mc));
+              const float e1 = fast_exp2(__builtin_fmaf(s[2 * st + 1], c, mc));
+              const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+              p.h[st / 4][2 * (st % 4)] = pr[0];
+              p.h[st / 4][2 * (st % 4) + 1] = pr[1];
+              rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
+              pin(rs);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            // Region B: PV(j) on the MFMA unit, row max of S(j+1) on the VALU.
+#pragma unroll
+            for (int j = 0; j < F::NPV; ++j) {
+              F::pv_mfma(vf[j % VPF], j, p, o);
+              if (j + VPF < F::NPV) vf[j % VPF] = F::template v_frag<RSV>(v_cur, kt, j + VPF, lane, u);
+              if constexpr (HN) {
+                m2 = fmaxf(m2, fmaxf(sn[2 * j], sn[2 * j + 1]));
+                pin(m2);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          };
+          // The part's last sub-tile also scores a "next" one, from a K
+          // buffer that holds stale keys; S(j+1) is then never used.  That
+          // costs one sub-tile of QK per part and keeps O out of a branch
+          // (where the compiler would copy all 64 accumulators).
+          body(std::true_type{});
+          l_run += rs;
+          mx = m2;
+          if (!last || has1) {
+            const Chunk& chn = last ? ch1 : ch0;
+            if (needs_mask(chn)) mx = mask_sub(sn, ktn, chn);
+          }
+        }
+      }
+      __syncthreads();
+      ch0 = ch1;
+      ch1 = ch2;
+      ch2 = ch3;
+    };
+    for (int ci = 0; ci < nc; ++ci) {
+      if constexpr (NKT % 2 == 0) {
+        step(ci, sa, sb);
+      } else {
+        step(ci, sa, sb);
+        if (++ci >= nc) break;
+        step(ci, sb, sa);
+      }
+    }
+  }
+
+  const float l = pair_sum(l_run);
+  if (!row_ok) return;
+  if (a.n_splits > 1) {
+    // Partial record: O unnormalised, then m and l.
+    float* rec = a.ws + (((int64_t)row * a.hq + head) * a.n_splits + part) * cev_attn_partial_floats(D);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = dt * 32 + 8 * q4 + 4 * u;
+        *(f32x4*)(rec + d) = f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
+      }
+    if (u == 0) *(f32x4*)(rec + D) = f32x4{m_run, l, 0.0f, 0.0f};
+    return;
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh : nullptr;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = dt * 32 + 8 * q4 + 4 * u;
+      float v[4], gv[4];
+      if (gp) load_vec4<T>(gp + d, gv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x = BF ? o[dt][4 * q4 + e] * inv : (l > 0.0f ? o[dt][4 * q4 + e] / l : 0.0f);
+        if (gp) x = gate_value(x, gv[e], BF);
+        v[e] = x;
+      }
+      store_vec4<T>(op + d, v);
+    }
+}
+
+// --------------------------------------------------------------------------
+// d = 256 and f32: one K/V chunk double-buffered in LDS, scored, then
+// multiplied into O, one barrier per chunk.  O and Q take 192 VGPRs at
+// d = 256 (Q alone 64 in f32), which leaves no room for a second score tile.
+template <typename T, int D>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
   using F = Frag<T, D>;
   constexpr bool BF = sizeof(T) == 2;
   constexpr int BN = F::BN;
@@ -240,6 +693,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
   constexpr int NLD = BN * D / VEC / NT;  // 16-byte loads per thread per tensor
   static_assert(BN * D / VEC % NT == 0, "tile loads must split evenly");
   typedef typename F::Vec Vec;
+  using P = typename F::P;
   __shared__ __align__(16) T smem[2 * TILE];
 
   if (!plan_ok(a)) return;
@@ -279,56 +733,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
   // ---- this part's slice of the tile's key stream: chunks [c0, c1)
   const int c0 = (int)((int64_t)part * n_chunks / a.n_splits);
   const int c1 = (int)((int64_t)(part + 1) * n_chunks / a.n_splits);
-  auto seg_of = [&](int s_i) { return clamp_seg(segs[s_i], a.s_cache, a.t); };
-  int si = 0, k0 = 0;
-  {
-    int cc = c0;
-    for (; si < nseg; ++si) {
-      const int4 sg = seg_of(si);
-      const int nch = (max(0, sg.y - sg.x) + BN - 1) / BN;
-      if (cc < nch) {
-        k0 = cc * BN;
-        break;
-      }
-      cc -= nch;
-    }
-  }
-  auto next = [&](int& s_i, int& s_k0) {
-    const int4 sg = seg_of(s_i);
-    s_k0 += BN;
-    if (sg.x + s_k0 < sg.y) return;
-    s_k0 = 0;
-    for (++s_i; s_i < nseg; ++s_i) {
-      const int4 s2 = seg_of(s_i);
-      if (s2.y > s2.x) return;
-    }
-  };
-
+  ChunkCursor<BN> cursor{segs, nseg, a.s_cache, a.t, 0, 0, make_int4(0, 0, 0, 0)};
+  cursor.seek(c0);
+  KvSource<T> kvs;
+  kvs.init(a, kvh);
   Vec kreg[NLD], vreg[NLD];
-  auto load = [&](int s_i, int s_k0) {
-    const int4 sg = seg_of(s_i);
-    const int key0 = sg.x + s_k0;
-    const int nvalid = min(BN, sg.y - key0);
-    const bool cached = key0 < a.s_cache;
-    const T* kb = cached ? (const T*)a.kc + kvh * a.kc_sh + (int64_t)key0 * a.kc_ss
-                         : (const T*)a.kn + kvh * a.kn_sh + (int64_t)(key0 - a.s_cache) * a.kn_st;
-    const T* vb = cached ? (const T*)a.vc + kvh * a.vc_sh + (int64_t)key0 * a.vc_ss
-                         : (const T*)a.vn + kvh * a.vn_sh + (int64_t)(key0 - a.s_cache) * a.vn_st;
-    const int64_t ks = cached ? a.kc_ss : a.kn_st;
-    const int64_t vs = cached ? a.vc_ss : a.vn_st;
-#pragma unroll
-    for (int r = 0; r < NLD; ++r) {
-      const int v = tid + r * NT;
-      const int key = v / (D / VEC), col = (v % (D / VEC)) * VEC;
-      Vec x = {}, y = {};
-      if (key < nvalid) {  // keys past the segment stay zero
-        x = *(const Vec*)(kb + (int64_t)key * ks + col);
-        y = *(const Vec*)(vb + (int64_t)key * vs + col);
-      }
-      kreg[r] = x;
-      vreg[r] = y;
-    }
-  };
+  auto load = [&](const Chunk& ch) { load_chunk<T, D, NLD, NT, Vec>(kvs, ch, tid, kreg, vreg); };
   auto store = [&](int buf) {
     T* sk = smem + buf * TILE;
     T* sv = sk + BN * RS;
@@ -342,77 +752,81 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a) {
   };
 
   const int my_chunks = c1 - c0;
-  if (my_chunks > 0 && si < nseg) {
-    load(si, k0);
+  if (my_chunks > 0 && cursor.valid()) {
+    Chunk ch = cursor.here();
+    load(ch);
     store(0);
     __syncthreads();
     int buf = 0;
     for (int ci = 0;; ++ci) {
-      int nsi = si, nk0 = k0;
-      next(nsi, nk0);
-      const bool more = ci + 1 < my_chunks && nsi < nseg;
-      if (more) load(nsi, nk0);  // in flight while this tile is scored
-
+      const bool more = ci + 1 < my_chunks;
+      Chunk chn{0, 0, 0};
+      if (more) {
+        cursor.next();
+        chn = cursor.here();
+        load(chn);  // in flight while this chunk is scored
+      }
       const T* sK = smem + buf * TILE;
       const T* sV = sK + BN * RS;
-      const int4 sg = seg_of(si);
-      const int key0 = sg.x + k0;
-      const int nvalid = min(BN, sg.y - key0);
+      const int key0 = ch.key0;
+      const int nvalid = ch.nvalid;
 
       if (wave_active) {
-      f32x16 s[NKT];
+        f32x16 s[NKT];
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt) s[kt] = fr.template qk<RS>(sK, kt, n, u);
-      if (sg.z != 0 || nvalid < BN) {
-        // Branch-free on purpose: a short-circuit && / || here gives every
-        // element its own control flow, and hipcc 7.2 then reuses the score
-        // register of element 0 for `key` and drops its select.
-        const bool all_rows = sg.z == 0;
+        for (int kt = 0; kt < NKT; ++kt) {
+          s[kt] = f32x16{};
+#pragma unroll
+          for (int st = 0; st < F::NQK; ++st) fr.template qk_step<RS>(sK, kt, st, n, u, s[kt]);
+        }
+        if (ch.local != 0 || nvalid < BN) {
+          // Branch-free on purpose: a short-circuit && / || here gives every
+          // element its own control flow, and hipcc 7.2 then reuses the
+          // score register of element 0 for `key` and drops its select.
+          const bool all_rows = ch.local == 0;
+#pragma unroll
+          for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int kk = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
+              const int key = key0 + kk;
+              const bool vis = (kk < nvalid) & (all_rows | ((key >= rv.x) & (key < rv.y)) | (key == rv.z));
+              s[kt][i] = vis ? s[kt][i] : -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int kk = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
-            const int key = key0 + kk;
-            const bool vis = (kk < nvalid) & (all_rows | ((key >= rv.x) & (key < rv.y)) | (key == rv.z));
-            s[kt][i] = vis ? s[kt][i] : -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+        const float m_cand = pair_max(mx) * c;
+        const bool grow = m_cand > m_run + kRescale;
+        if (__ballot(grow)) {
+          const float m_new = grow ? m_cand : m_run;
+          const float alpha = fast_exp2(m_run - m_new);
+          m_run = m_new;
+          l_run *= alpha;
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
-      const float m_cand = pair_max(mx) * c;
-      const bool grow = m_cand > m_run + kRescale;
-      if (__ballot(grow)) {
-        const float m_new = grow ? m_cand : m_run;
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
-      }
-      float rs = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float p = fast_exp2(__builtin_fmaf(s[kt][i], c, -m_run));
-          s[kt][i] = p;
-          rs += p;
+          for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
         }
-      l_run += rs;
+        float rs = 0.0f;
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt) fr.template pv<RSV>(sV, kt, lane, u, s[kt], o);
+        for (int kt = 0; kt < NKT; ++kt) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[kt][i] = fast_exp2(__builtin_fmaf(s[kt][i], c, -m_run));
+          P p;
+          F::make_p(s[kt], p, rs);
+#pragma unroll
+          for (int j = 0; j < F::NPV; ++j) fr.template pv_step<RSV>(sV, kt, j, lane, u, p, o);
+        }
+        l_run += rs;
       }
 
       if (!more) break;
       store(buf ^ 1);  // that buffer was last read before the previous barrier
       __syncthreads();
       buf ^= 1;
-      si = nsi;
-      k0 = nk0;
+      ch = chn;
     }
   }
 
@@ -538,7 +952,10 @@ template <typename T, int D>
 int32_t launch(const AttnArgs& a, hipStream_t stream) {
   const int64_t grid = (int64_t)a.n_tiles * a.n_splits * a.hkv;
   if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "grid of %lld workgroups is too large", (long long)grid);
-  hipLaunchKernelGGL((attn_kernel<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
+  if constexpr (sizeof(T) == 2 && D == 128)
+    hipLaunchKernelGGL((attn_kernel_pipe<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attn_kernel_seq<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "packed attention launch: %s", hipGetErrorString(e));
   if (a.n_splits > 1) {
