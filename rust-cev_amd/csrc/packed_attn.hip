@@ -386,33 +386,131 @@ __device__ __forceinline__ void load_chunk(const KvSource<T>& src, const Chunk& 
 // overlap inside each wave (the loop below says how).  Two waves share a
 // SIMD at 256 VGPRs, and the per-chunk barrier keeps them in step, so a
 // wave cannot rely on the other one to fill its idle issue slots.
+//
+// K/V chunks go from HBM straight into LDS (buffer_load ... lds), NBUF
+// chunk buffers deep, so up to NBUF-2 chunks are in flight per workgroup
+// without holding registers.  Tiles are unpadded, 256 bytes a key row, with
+// the 16-byte column blocks of a row permuted so the operand reads are free
+// of bank conflicts:
+//   K: block c of row r at slot c ^ (r & 15)   (ds_read_b128, one key row
+//      per lane, 16 rows per 256 bytes read)
+//   V: block c of row r at slot c ^ 4(r & 3)   (ds_read_b64_tr_b16, four
+//      rows x four blocks per 16 lanes)
+namespace pipe {
+constexpr int kBuf = 4;             // chunk buffers
+constexpr int kAhead = kBuf - 1;    // chunk i + kAhead is fetched in iteration i
+constexpr int kRowBytes = 256;      // one bf16 key row of d = 128
+constexpr int kTileBytes = 64 * kRowBytes;
+constexpr int kVBase = kBuf * kTileBytes;  // K tiles first, then V tiles
+
+__device__ __forceinline__ int k_slot(int blk, int row) { return blk ^ (row & 15); }
+__device__ __forceinline__ int v_slot(int blk, int row) { return blk ^ ((row & 3) << 2); }
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <typename Fn, int... I>
+__device__ __forceinline__ void static_for_impl(Fn&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N-1>).
+template <int N, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// V^T operand reads.  The compiler places an s_waitcnt vmcnt(0) before
+// every ds_read_b64_tr_b16 it emits while an LDS DMA is in flight (it
+// cannot tell the buffers apart), which would drain the whole fetch
+// pipeline once per sub-tile.  These reads are issued from asm instead;
+// buffer reuse is ordered by the explicit vmcnt wait and barrier at the end
+// of each iteration, and wait_tr() below makes a fragment's registers
+// depend on the reads having returned.
+template <int OFF>
+__device__ __forceinline__ i32x2 read_tr(int vaddr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(vaddr), "i"(OFF) : "memory");
+  return r;
+}
+// The K operand reads go through asm as well, so that every LDS read in the
+// loop body is one whose position the waits below can count.
+template <int OFF>
+__device__ __forceinline__ i32x4 read_b128(int vaddr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  i32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(vaddr), "i"(OFF) : "memory");
+  return r;
+}
+// LDS returns in order: once at most N LGKM operations are outstanding,
+// every LDS read issued before the last N LDS reads has landed (an older
+// scalar load still in flight only makes the wait stricter).
+template <int N>
+__device__ __forceinline__ void wait_tr(i32x2& lo, i32x2& hi) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(lo), "+v"(hi) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void wait_b128(i32x4& r) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
+}
+
+// Issue order of the LDS reads of one sub-tile body (8 QK units, 8 PV
+// units, KPF = VPF = 3): three K reads up front; QK unit u then issues K
+// read u+3 (u < 5) or V fragment u-5 (u >= 5, two reads); PV unit j issues
+// V fragment j+3 (j < 5).  Each count below is the number of reads issued
+// after the one a unit waits for, up to that unit's wait.
+constexpr int kIssuedA(int u) { return (u + 3 < 8 ? 1 : 0) + (u >= 5 ? 2 : 0); }
+constexpr int kIssuedB(int j) { return j + 3 < 8 ? 2 : 0; }
+constexpr int kBeforeA(int st) {  // reads issued before QK unit st waits
+  int t = 3;
+  for (int u = 0; u < st; ++u) t += kIssuedA(u);
+  return t;
+}
+constexpr int kPosK(int st) {  // issue position of K read st
+  if (st < 3) return st;
+  int t = 3;
+  for (int u = 0; u < st - 3; ++u) t += kIssuedA(u);
+  return t;
+}
+constexpr int kWaitA(int st) { return kBeforeA(st) - kPosK(st) - 1; }
+constexpr int kPosVhi(int j) {  // issue position of the second read of V fragment j
+  if (j < 3) return kBeforeA(5 + j) + 1;
+  int t = kBeforeA(8);
+  for (int b = 0; b < j - 3; ++b) t += kIssuedB(b);
+  return t + 1;
+}
+constexpr int kWaitB(int j) {
+  int t = kBeforeA(8);
+  for (int b = 0; b < j; ++b) t += kIssuedB(b);
+  return t - kPosVhi(j) - 1;
+}
+static_assert(kWaitA(0) == 2 && kWaitA(5) == 2 && kWaitA(6) == 3 && kWaitA(7) == 4, "QK wait counts");
+static_assert(kWaitB(0) == 4 && kWaitB(5) == 4 && kWaitB(6) == 2 && kWaitB(7) == 0, "PV wait counts");
+}  // namespace pipe
+
 template <typename T, int D>
 __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_kernel_pipe(AttnArgs a) {
   using F = Frag<T, D>;
   using P = typename F::P;
-  constexpr bool BF = sizeof(T) == 2;
   constexpr int BN = F::BN;
-  constexpr int NT = kAttnWaves * 64;
-  constexpr int VEC = F::VEC;
-  constexpr int RS = D + F::PAD;    // LDS row stride (elements) of a K tile
-  constexpr int RSV = D + F::VPAD;  // LDS row stride of a V tile
-  constexpr int KT = BN * RS;
-  constexpr int VT = BN * RSV;
   constexpr int NKT = BN / 32;    // 32-key sub-tiles per chunk
   constexpr int NDT = D / 32;     // 32-wide slices of the head dim
-  constexpr int NLD = BN * D / VEC / NT;  // 16-byte loads per thread per tensor
-  constexpr int EPQ = 16 / F::NQK;        // exponentials per QK step
-  constexpr int MPV = 16 / F::NPV;        // max operands per PV step
-  static_assert(BN * D / VEC % NT == 0, "tile loads must split evenly");
-  static_assert(EPQ * F::NQK == 16 && MPV * F::NPV == 16, "interleave must cover a sub-tile");
-  static_assert(BF && D == 128, "the pipelined loop is sized for bf16, d = 128");
-  typedef typename F::Vec Vec;
-  __shared__ __align__(16) T smem[3 * KT + 3 * VT];
-  T* const kbuf = smem;
-  T* const vbuf = smem + 3 * KT;
+  static_assert(sizeof(T) == 2 && D == 128 && BN == 64 && kAttnWaves == 8, "the pipelined loop is sized for bf16, d = 128");
+  static_assert(F::NQK == 8 && F::NPV == 8, "unit layout below");
+  using namespace pipe;
+  __shared__ __align__(16) char lds[2 * kBuf * kTileBytes];
 
   if (!plan_ok(a)) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform_i32(tid >> 6);
   const int n = lane & 31, u = lane >> 5;
   const int kvh = blockIdx.x % a.hkv;
   const int item = blockIdx.x / a.hkv;
@@ -425,7 +523,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   const int4* rows = (const int4*)(a.plan + ph->rows_off);
   // Query slot (wave, n) holds row slot / g of the tile, query head slot % g:
   // the valid rows of a short tile fill the first waves, and a wave with no
-  // valid row skips the MFMA work (it still helps stage K/V).
+  // valid row skips the MFMA work (it still fetches its share of K/V).
   const int slot = wave * 32 + n;
   const int gi = slot % a.g;
   const int head = kvh * a.g + gi;
@@ -448,104 +546,156 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   // ---- this part's slice of the tile's key stream: chunks [c0, c1)
   const int c0 = (int)((int64_t)part * n_chunks / a.n_splits);
   const int c1 = (int)((int64_t)(part + 1) * n_chunks / a.n_splits);
+  const int nc = c1 - c0;
   ChunkCursor<BN> cursor{segs, nseg, a.s_cache, a.t, 0, 0, make_int4(0, 0, 0, 0)};
   cursor.seek(c0);
-  KvSource<T> kvs;
-  kvs.init(a, kvh);
-  Vec kreg[NLD], vreg[NLD];
-  auto load = [&](const Chunk& ch) { load_chunk<T, D, NLD, NT, Vec>(kvs, ch, tid, kreg, vreg); };
-  auto store = [&](T* sk, T* sv) {
-#pragma unroll
-    for (int r = 0; r < NLD; ++r) {
-      const int v = tid + r * NT;
-      const int key = v / (D / VEC), col = (v % (D / VEC)) * VEC;
-      *(Vec*)&sk[key * RS + col] = kreg[r];
-      *(Vec*)&sv[key * RSV + col] = vreg[r];
-    }
-  };
-  auto needs_mask = [](const Chunk& ch) { return ch.local != 0 || ch.nvalid < BN; };
-  // Masks sub-tile kt of chunk ch in place and returns its lane-local max.
-  auto mask_sub = [&](f32x16& s, int kt, const Chunk& ch) {
-    // Branch-free on purpose: a short-circuit && / || here gives every
-    // element its own control flow, and hipcc 7.2 then reuses the score
-    // register of element 0 for `key` and drops its select.
-    const bool all_rows = ch.local == 0;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kk = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
-      const int key = ch.key0 + kk;
-      const bool vis = (kk < ch.nvalid) & (all_rows | ((key >= rv.x) & (key < rv.y)) | (key == rv.z));
-      s[i] = vis ? s[i] : -INFINITY;
-      mx = fmaxf(mx, s[i]);
-    }
-    return mx;
-  };
+  if (nc <= 0 || !cursor.valid()) {
+    // no key visible to this part: empty record / zero rows below
+  } else {
+    KvSource<T> kvs;
+    kvs.init(a, kvh);
 
-  // ---- main loop, software-pipelined over 32-key sub-tiles j:
-  //   scores S(j+1) = K(j+1) . Q^T run on the MFMA unit while the VALU turns
-  //   S(j) into probabilities; then O += V(j)^T . P(j) runs while the VALU
-  //   takes the row max of S(j+1).  The softmax max and the lazy rescale
-  //   are per sub-tile.  K and V tiles are triple-buffered in LDS: during
-  //   iteration i the waves read K of chunks i and i+1 and V of chunk i
-  //   while chunk i+2 is written into the buffers chunk i-1 used; chunk
-  //   i+3 is fetched into registers during iteration i, so one barrier per
-  //   chunk orders every LDS reuse.
-  const int nc = c1 - c0;
-  if (nc > 0 && cursor.valid()) {
-    Chunk ch1{0, 0, 0}, ch2{0, 0, 0}, ch3{0, 0, 0};  // chunks i+1, i+2, i+3
-    Chunk ch0 = cursor.here();                       // chunk i
-    load(ch0);
-    store(kbuf, vbuf);
-    if (nc > 1) {
-      cursor.next();
-      ch1 = cursor.here();
-      load(ch1);
-      store(kbuf + KT, vbuf + VT);
+    // Per-lane byte offsets of the operand reads inside a tile; the
+    // sub-tile, half and buffer parts are immediates.
+    int koff[F::NQK], voff[NDT];
+#pragma unroll
+    for (int st = 0; st < F::NQK; ++st) koff[st] = n * kRowBytes + (k_slot(2 * st + u, n) << 4);
+    {
+      const int i = lane & 15, g16 = (lane >> 4) & 1, rr = i >> 2;
+      const int blk = 2 * g16 + ((i & 3) >> 1);  // 16-byte block of the read, within a 64-byte slice
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+        voff[dt] = kVBase + (4 * u + rr) * kRowBytes + (v_slot(4 * dt + blk, rr) << 4) + 8 * (i & 1);
     }
-    if (nc > 2) {
-      cursor.next();
-      ch2 = cursor.here();
-      load(ch2);
-    }
+    auto k_frag = [&](int buf, int kt, int st) {
+      return *(const bf16x8*)(lds + koff[st] + buf * kTileBytes + kt * 32 * kRowBytes);
+    };
+    // V^T fragment j (h = j / 4, head-dim slice dt = j % 4) of sub-tile KT in
+    // buffer BUF: the transpose reads of rows r and r + 8.
+    const int lds_base = (int)(size_t)(const __attribute__((address_space(3))) char*)lds;
+    struct VFrag {
+      i32x2 lo, hi;
+    };
+    auto v_issue = [&](auto buf_c, auto kt_c, auto j_c) {
+      constexpr int BUF = decltype(buf_c)::value, KT = decltype(kt_c)::value, J = decltype(j_c)::value;
+      constexpr int OFF = BUF * kTileBytes + (KT * 32 + 16 * (J / NDT)) * kRowBytes;
+      const int va = lds_base + voff[J % NDT];
+      return VFrag{read_tr<OFF>(va), read_tr<OFF + 8 * kRowBytes>(va)};
+    };
+    auto v_ready = [](VFrag& f, auto j_c) {
+      wait_tr<kWaitB(decltype(j_c)::value)>(f.lo, f.hi);
+      const bf16x4 lo = __builtin_bit_cast(bf16x4, f.lo), hi = __builtin_bit_cast(bf16x4, f.hi);
+      return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    // K fragment st of sub-tile KT in buffer BUF.
+    auto k_issue = [&](auto buf_c, auto kt_c, auto st_c) {
+      constexpr int OFF = decltype(buf_c)::value * kTileBytes + decltype(kt_c)::value * 32 * kRowBytes;
+      return read_b128<OFF>(lds_base + koff[decltype(st_c)::value]);
+    };
+    auto k_ready = [](i32x4& r, auto st_c) {
+      wait_b128<kWaitA(decltype(st_c)::value)>(r);
+      return __builtin_bit_cast(bf16x8, r);
+    };
+
+    // Chunk ch into buffer buf: each wave fetches rows 8w .. 8w+7 of K and
+    // of V, four rows (1 KB) per instruction; rows past the chunk's last
+    // valid key read as zero.
+    auto fetch = [&](const Chunk& ch, int buf) {
+      __amdgpu_buffer_rsrc_t rk, rvs;
+      int kr, vr;
+      kvs.rsrc(ch, rk, rvs, kr, vr);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int krow = 8 * wave + 4 * r + (lane >> 4), blk = lane & 15;
+        const int kdst = buf * kTileBytes + (8 * wave + 4 * r) * kRowBytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(lds + kdst), 16,
+                                                 krow * kr + (k_slot(blk, krow) << 4), 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rvs, (__attribute__((address_space(3))) void*)(lds + kVBase + kdst), 16,
+                                                 krow * vr + (v_slot(blk, krow) << 4), 0, 0, 0);
+      }
+    };
+    constexpr int kLoadsPerChunk = 4;  // buffer_load ... lds per wave per chunk
+
+    auto needs_mask = [](const Chunk& ch) { return ch.local != 0 || ch.nvalid < BN; };
+    // Masks sub-tile kt of chunk ch in place and returns its lane-local max.
+    auto mask_sub = [&](f32x16& s, int kt, const Chunk& ch) {
+      // Branch-free on purpose: a short-circuit && / || here gives every
+      // element its own control flow, and hipcc 7.2 then reuses the score
+      // register of element 0 for `key` and drops its select.
+      const bool all_rows = ch.local == 0;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kk = kt * 32 + 8 * (i >> 2) + 4 * u + (i & 3);
+        const int key = ch.key0 + kk;
+        const bool vis = (kk < ch.nvalid) & (all_rows | ((key >= rv.x) & (key < rv.y)) | (key == rv.z));
+        s[i] = vis ? s[i] : -INFINITY;
+        mx = fmaxf(mx, s[i]);
+      }
+      return mx;
+    };
+
+    // Stale LDS must hold finite values: a masked key's V row is multiplied
+    // by p = 0.  Zero every buffer once before the first fetch.
+    for (int i = tid; i < 2 * kBuf * kTileBytes / 16; i += kAttnWaves * 64) *(f32x4*)(lds + 16 * i) = f32x4{};
     __syncthreads();
+
+    // chs[k] is chunk i + k of the part; chunks past its end are empty
+    // (their fetch reads no memory).
+    int produced = 0;
+    auto next_chunk = [&]() {
+      Chunk ch{0, 0, 0};
+      if (produced < nc) {
+        if (produced > 0) cursor.next();
+        ch = cursor.here();
+      }
+      ++produced;
+      return ch;
+    };
+    Chunk chs[kAhead + 1];
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) {
+      chs[k] = next_chunk();
+      fetch(chs[k], k);
+    }
+    wait_vmcnt<kLoadsPerChunk * (kAhead - 2)>();  // chunks 0 and 1 landed
+    __builtin_amdgcn_s_barrier();
+
     f32x16 sa, sb;
     float mx = -INFINITY;  // lane-local max of the current sub-tile
     if (wave_active) {
       sa = f32x16{};
 #pragma unroll
-      for (int st = 0; st < F::NQK; ++st) fr.template qk_step<RS>(kbuf, 0, st, n, u, sa);
-      if (needs_mask(ch0)) {
-        mx = mask_sub(sa, 0, ch0);
+      for (int st = 0; st < F::NQK; ++st) fr.qk_mfma(k_frag(0, 0, st), st, sa);
+      if (needs_mask(chs[0])) {
+        mx = mask_sub(sa, 0, chs[0]);
       } else {
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sa[i]);
       }
     }
 
-    // One chunk; on entry s_in holds S of its first sub-tile.
-    auto step = [&](int ci, f32x16& s_in, f32x16& s_other) {
-      const bool has1 = ci + 1 < nc, has2 = ci + 2 < nc, has3 = ci + 3 < nc;
-      const int b0 = ci % 3, b1 = b0 == 2 ? 0 : b0 + 1, b2 = b1 == 2 ? 0 : b1 + 1;  // buffers of chunks ci, ci+1, ci+2
-      const T* k_cur = kbuf + b0 * KT;
-      const T* k_next = kbuf + b1 * KT;
-      const T* v_cur = vbuf + b0 * VT;
-      // chunk ci+2 into the buffers chunk ci-1 used: its last reads were
-      // before the previous barrier
-      if (has2) store(kbuf + b2 * KT, vbuf + b2 * VT);
-      if (has3) {
-        cursor.next();
-        ch3 = cursor.here();
-        load(ch3);
-      }
+    // ---- main loop, software-pipelined over 32-key sub-tiles j:
+    //   scores S(j+1) = K(j+1) . Q^T run on the MFMA unit while the VALU
+    //   turns S(j) into probabilities; then O += V(j)^T . P(j) runs while
+    //   the VALU takes the row max of S(j+1).  The softmax max and the lazy
+    //   rescale are per sub-tile.  Iteration i reads K of chunks i and i+1
+    //   and V of chunk i, fetches chunk i + kAhead into the buffer chunk
+    //   i-1 used, and before its barrier waits for chunk i+2 to land.
+    auto step = [&](int ci, auto buf_tag) {
+      constexpr int B0 = decltype(buf_tag)::value;  // buffer of chunk ci
+      constexpr int B1 = (B0 + 1) % kBuf;
+      const bool has1 = ci + 1 < nc;
+      chs[kAhead] = next_chunk();
+      fetch(chs[kAhead], (B0 + kAhead) % kBuf);
       if (wave_active) {
-#pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-          f32x16& s = kt % 2 == 0 ? s_in : s_other;
-          f32x16& sn = kt % 2 == 0 ? s_other : s_in;
-          const bool last = kt + 1 == NKT;
-          const T* kn_ptr = last ? k_next : k_cur;
-          const int ktn = last ? 0 : kt + 1;
+        static_for<NKT>([&](auto kt_c) {
+          constexpr int kt = decltype(kt_c)::value;
+          f32x16& s = kt % 2 == 0 ? sa : sb;
+          f32x16& sn = kt % 2 == 0 ? sb : sa;
+          constexpr bool last = kt + 1 == NKT;
+          constexpr int bn = last ? B1 : B0;  // buffer and sub-tile of the next scores
+          constexpr int ktn = last ? 0 : kt + 1;
           // lazy rescale against this sub-tile's row max
           {
             const float m_cand = pair_max(mx) * c;
@@ -561,82 +711,83 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
           }
           const float mc = -m_run;
           float rs = 0.0f, m2 = -INFINITY;
-          // One straight-line block per case, so the scheduler pairs the
-          // MFMAs of one stream with the VALU work of the other.
-          auto body = [&](auto has_next_tag) {
-            constexpr bool HN = decltype(has_next_tag)::value;
-            constexpr int KPF = 3;  // K fragments in flight ahead of their MFMA
-            constexpr int VPF = 3;  // V fragments in flight ahead of their MFMA
-            static_assert(EPQ == 2 && MPV == 2 && F::NQK == 8 && F::NPV == 8, "unit layout below");
-            // Each unit below ends in a scheduling fence, so the order is
-            // the program order unit by unit: one MFMA of one stream next to
-            // the VALU work of the other, with operand reads KPF / VPF units
-            // ahead of their MFMA.
-            bf16x8 kf[KPF], vf[VPF];
-            P p;
-            if constexpr (HN) {
-              sn = f32x16{};
-#pragma unroll
-              for (int f = 0; f < KPF; ++f) kf[f] = F::template k_frag<RS>(kn_ptr, ktn, f, n, u);
-            }
-            const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-            // Region A: QK(j+1) on the MFMA unit; exp(j), P(j) and its row sum
-            // on the VALU, two probabilities per unit.
-#pragma unroll
-            for (int st = 0; st < F::NQK; ++st) {
-              if constexpr (HN) {
-                fr.qk_mfma(kf[st % KPF], st, sn);
-                if (st + KPF < F::NQK) kf[st % KPF] = F::template k_frag<RS>(kn_ptr, ktn, st + KPF, n, u);
-              }
-              if (st >= F::NQK - VPF) vf[st - (F::NQK - VPF)] = F::template v_frag<RSV>(v_cur, kt, st - (F::NQK - VPF), lane, u);
-              const float e0 = fast_exp2(__builtin_fmaf(s[2 * st], c, mc));
-              const float e1 = fast_exp2(__builtin_fmaf(s[2 * st + 1], c, mc));
-              const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
-              p.h[st / 4][2 * (st % 4)] = pr[0];
-              p.h[st / 4][2 * (st % 4) + 1] = pr[1];
-              rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
-              pin(rs);
-              __builtin_amdgcn_sched_barrier(0);
-            }
-            // Region B: PV(j) on the MFMA unit, row max of S(j+1) on the VALU.
-#pragma unroll
-            for (int j = 0; j < F::NPV; ++j) {
-              F::pv_mfma(vf[j % VPF], j, p, o);
-              if (j + VPF < F::NPV) vf[j % VPF] = F::template v_frag<RSV>(v_cur, kt, j + VPF, lane, u);
-              if constexpr (HN) {
-                m2 = fmaxf(m2, fmaxf(sn[2 * j], sn[2 * j + 1]));
-                pin(m2);
-              }
-              __builtin_amdgcn_sched_barrier(0);
-            }
-          };
-          // The part's last sub-tile also scores a "next" one, from a K
-          // buffer that holds stale keys; S(j+1) is then never used.  That
-          // costs one sub-tile of QK per part and keeps O out of a branch
-          // (where the compiler would copy all 64 accumulators).
-          body(std::true_type{});
+          constexpr int KPF = 3;  // K fragments in flight ahead of their MFMA
+          constexpr int VPF = 3;  // V fragments in flight ahead of their MFMA
+          // Each unit below ends in a scheduling fence, so the order is the
+          // program order unit by unit: one MFMA of one stream next to the
+          // VALU work of the other, with operand reads KPF / VPF units ahead
+          // of their MFMA.  The part's last sub-tile also scores a "next"
+          // one from a buffer of stale or zero keys, never used: that keeps
+          // O out of a branch (where the compiler copies all 64 accumulators).
+          static_assert(KPF == 3 && VPF == 3, "the wait counts assume three fragments ahead");
+          using BN_c = std::integral_constant<int, bn>;
+          using KTN_c = std::integral_constant<int, ktn>;
+          i32x4 kf[KPF];
+          VFrag vf[VPF];
+          P p;
+          sn = f32x16{};
+          static_for<KPF>([&](auto f_c) { kf[decltype(f_c)::value] = k_issue(BN_c{}, KTN_c{}, f_c); });
+          const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+          // Region A: QK(j+1) on the MFMA unit; exp(j), P(j) and its row sum
+          // on the VALU, two probabilities per unit.  Its last VPF units
+          // issue the first V fragments of region B.
+          static_for<F::NQK>([&](auto st_c) {
+            constexpr int st = decltype(st_c)::value;
+            fr.qk_mfma(k_ready(kf[st % KPF], st_c), st, sn);
+            if constexpr (st + KPF < F::NQK) kf[st % KPF] = k_issue(BN_c{}, KTN_c{}, std::integral_constant<int, st + KPF>{});
+            if constexpr (st >= F::NQK - VPF)
+              vf[st - (F::NQK - VPF)] = v_issue(std::integral_constant<int, B0>{}, kt_c, std::integral_constant<int, st - (F::NQK - VPF)>{});
+            const float e0 = fast_exp2(__builtin_fmaf(s[2 * st], c, mc));
+            const float e1 = fast_exp2(__builtin_fmaf(s[2 * st + 1], c, mc));
+            const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+            p.h[st / 4][2 * (st % 4)] = pr[0];
+            p.h[st / 4][2 * (st % 4) + 1] = pr[1];
+            rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
+            pin(rs);
+            __builtin_amdgcn_sched_barrier(0);
+          });
+          // Region B: PV(j) on the MFMA unit, row max of S(j+1) on the VALU.
+          static_for<F::NPV>([&](auto j_c) {
+            constexpr int j = decltype(j_c)::value;
+            F::pv_mfma(v_ready(vf[j % VPF], j_c), j, p, o);
+            if constexpr (j + VPF < F::NPV)
+              vf[j % VPF] = v_issue(std::integral_constant<int, B0>{}, kt_c, std::integral_constant<int, j + VPF>{});
+            m2 = fmaxf(m2, fmaxf(sn[2 * j], sn[2 * j + 1]));
+            pin(m2);
+            __builtin_amdgcn_sched_barrier(0);
+          });
           l_run += rs;
           mx = m2;
           if (!last || has1) {
-            const Chunk& chn = last ? ch1 : ch0;
+            const Chunk& chn = last ? chs[1] : chs[0];
             if (needs_mask(chn)) mx = mask_sub(sn, ktn, chn);
           }
-        }
+        });
       }
-      __syncthreads();
-      ch0 = ch1;
-      ch1 = ch2;
-      ch2 = ch3;
+      // Chunk ci+2 (fetched in iteration ci-1) must have landed before the
+      // barrier; chunk ci + kAhead may stay in flight.
+      wait_vmcnt<kLoadsPerChunk * (kAhead - 2)>();
+      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int k = 0; k < kAhead; ++k) chs[k] = chs[k + 1];
     };
-    for (int ci = 0; ci < nc; ++ci) {
-      if constexpr (NKT % 2 == 0) {
-        step(ci, sa, sb);
-      } else {
-        step(ci, sa, sb);
-        if (++ci >= nc) break;
-        step(ci, sb, sa);
-      }
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    static_assert(kBuf == 4, "the unrolled loop below walks four buffers");
+    for (int ci = 0; ci < nc; ci += kBuf) {
+      step(ci, I0{});
+      if (ci + 1 >= nc) break;
+      step(ci + 1, I1{});
+      if (ci + 2 >= nc) break;
+      step(ci + 2, I2{});
+      if (ci + 3 >= nc) break;
+      step(ci + 3, I3{});
     }
+    // Fetches past the part's end read no memory, but they still write
+    // zeros into LDS: drain them before the workgroup exits.
+    wait_vmcnt<0>();
   }
 
   const float l = pair_sum(l_run);
@@ -666,8 +817,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
       if (gp) load_vec4<T>(gp + d, gv);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float x = BF ? o[dt][4 * q4 + e] * inv : (l > 0.0f ? o[dt][4 * q4 + e] / l : 0.0f);
-        if (gp) x = gate_value(x, gv[e], BF);
+        float x = o[dt][4 * q4 + e] * inv;
+        if (gp) x = gate_value(x, gv[e], true);
         v[e] = x;
       }
       store_vec4<T>(op + d, v);
