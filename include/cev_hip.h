@@ -183,6 +183,49 @@ int32_t cev_qknorm_rope(const cev_qknorm_desc* d, const void* q_in, const void* 
 int32_t cev_rope_table(double theta, int32_t rotary_dim, int32_t n_pos, int32_t dtype, void* cos, void* sin);
 
 /* ------------------------------------------------------------------ */
+/* Gated DeltaNet layer core (Qwen3.5 linear-attention layers): replaces
+ * GatedDeltaNet::forward (crates/cev-model/src/qwen35.rs:414-453) between
+ * the input projections and out_proj, i.e. the depthwise conv + SiLU with
+ * its state (qwen35.rs:424-428, decoder.rs:137-151), l2norm / sigmoid /
+ * softplus gates, chunk_gated_delta_rule (qwen35.rs:301-368) and the gated
+ * RMSNorm (qwen35.rs:443-449). */
+typedef struct cev_gdn_desc {
+  int32_t dtype;       /* model dtype: projections, conv weight, conv state, y */
+  int32_t batch;       /* rows B */
+  int32_t t;           /* tokens per row */
+  int32_t n_k_heads;   /* linear_num_key_heads */
+  int32_t n_v_heads;   /* linear_num_value_heads, a multiple of n_k_heads */
+  int32_t head_k_dim;  /* 128 */
+  int32_t head_v_dim;  /* 128 */
+  int32_t conv_kernel; /* linear_conv_kernel_dim, 2..8 */
+  float eps;           /* rms_norm_eps of the gated norm */
+  int32_t reserved;
+  /* element strides; the channel stride is 1 */
+  int64_t mixed_stride_b, mixed_stride_t; /* in_proj_qkv output (B, T, 2 nk dk + nv dv) */
+  int64_t z_stride_b, z_stride_t;         /* in_proj_z output (B, T, nv dv) */
+  int64_t ab_stride_b, ab_stride_t;       /* in_proj_b / in_proj_a outputs (B, T, nv) */
+  int64_t conv_in_stride_b;               /* conv state (B, conv_dim, K-1); 0 broadcasts one state */
+  int64_t s_in_stride_b;                  /* recurrent state (B, nv, dk, dv) f32; 0 broadcasts */
+  int64_t y_stride_b, y_stride_t;         /* output (B, T, nv dv) */
+} cev_gdn_desc;
+
+/* Fills d with contiguous strides and validates it. */
+int32_t cev_gdn_desc_init(cev_gdn_desc* d, int32_t dtype, int32_t batch, int32_t t, int32_t n_k_heads, int32_t n_v_heads,
+                          int32_t head_k_dim, int32_t head_v_dim, int32_t conv_kernel, float eps);
+int32_t cev_gdn_workspace_size(const cev_gdn_desc* d, size_t* bytes);
+
+/* One layer for B rows of T tokens.  mixed, z, b, a, conv_w (conv_dim, K),
+ * conv_in and y are in the model dtype; neg_a = -exp(A_log), dt_bias and
+ * norm_w are f32 (as GatedDeltaNet::new holds them, qwen35.rs:393-395);
+ * s_in / s_out are (B, nv, dk, dv) f32.  conv_in == NULL / s_in == NULL
+ * start from zero state (qwen35.rs:422).  conv_out is (B, conv_dim, K-1)
+ * contiguous.  Workspace of cev_gdn_workspace_size bytes, 256-byte
+ * aligned. */
+int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, const void* z, const void* b, const void* a, const void* conv_w,
+                        const float* neg_a, const float* dt_bias, const float* norm_w, const void* conv_in, const float* s_in, void* y,
+                        void* conv_out, float* s_out, void* workspace, size_t workspace_bytes, cev_stream stream);
+
+/* ------------------------------------------------------------------ */
 /* Table builders (host only). */
 
 /* The packed pass of engine.rs:365-442.  Plans p = 0..n_plans-1 in plan

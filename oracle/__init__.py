@@ -80,6 +80,7 @@ def _declare(L):
         "orc_chunk_gated_delta_rule": (v, [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_void_p, i, i, i, i, i, _f32p, _f32p]),
         "orc_gdn_recurrence": (v, [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_void_p, i, i, i, i, _f32p, _f32p]),
         "orc_conv_silu": (v, [_f32p, C.c_void_p, _f32p, i, i, i, i, _f32p, _f32p]),
+        "orc_gated_rmsnorm": (v, [_f32p, _f32p, _f32p, i64, i, f, i, _f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -324,3 +325,47 @@ def conv_silu(x, tail, w, bf16: bool):
     lib().orc_conv_silu(x.reshape(-1), None if tc is None else tc.ctypes.data, _c(w).reshape(-1), c, t, kw, int(bf16),
                         y.reshape(-1), nt.reshape(-1))
     return y, nt
+
+
+def gated_rmsnorm(core, z, w, eps: float, bf16: bool):
+    """qwen35.rs:443-449: core / sqrt(mean core^2 + eps) * w * silu(z), rows of dv."""
+    core, z, w = _c(core), _c(z), _c(w)
+    dv = core.shape[-1]
+    y = np.empty_like(core)
+    lib().orc_gated_rmsnorm(core.reshape(-1), z.reshape(-1), w, core.size // dv, dv, float(eps), int(bf16), y.reshape(-1))
+    return y
+
+
+def softplus_vec(x):
+    return np.array([softplus(float(v)) for v in np.asarray(x, np.float32).reshape(-1)], np.float32).reshape(np.shape(x))
+
+
+def gdn_layer(mixed, z, b, a, conv_w, neg_a, dt_bias, norm_w, nk: int, nv: int, dk: int, dv: int, eps: float, bf16: bool,
+              conv_in=None, s_in=None):
+    """GatedDeltaNet::forward (qwen35.rs:414-453) from the projection outputs on:
+    mixed (B, T, 2 nk dk + nv dv), z (B, T, nv dv), b / a (B, T, nv) as f32 arrays
+    holding model-dtype values; conv_w (C, K); neg_a = -exp(A_log), dt_bias,
+    norm_w f32; conv_in (B, C, K-1) or None; s_in (B, nv, dk, dv) or None.
+    Returns y (B, T, nv dv) before out_proj, the new conv tail and state."""
+    B, T, Cd = mixed.shape
+    kd = nk * dk
+    ys, tails, states = [], [], []
+    for r in range(B):
+        x = np.ascontiguousarray(mixed[r].T)  # (C, T)
+        conved, tail = conv_silu(x, None if conv_in is None else conv_in[r], conv_w, bf16)
+        conved = conved.T  # (T, C)
+        q = conved[:, :kd].reshape(T, nk, dk).transpose(1, 0, 2)
+        k = conved[:, kd:2 * kd].reshape(T, nk, dk).transpose(1, 0, 2)
+        v = conved[:, 2 * kd:].reshape(T, nv, dv).transpose(1, 0, 2)
+        rep = nv // nk
+        q = np.repeat(q, rep, axis=0)
+        k = np.repeat(k, rep, axis=0)
+        beta = (1.0 / (1.0 + np.exp(-b[r].astype(np.float32)))).astype(np.float32).T  # (nv, T)
+        g = (softplus_vec(a[r].astype(np.float32) + dt_bias[None, :]) * neg_a[None, :]).astype(np.float32).T
+        core, s = chunk_gated_delta_rule(q, k, v, g, beta, None if s_in is None else s_in[r])
+        core = core.transpose(1, 0, 2).reshape(T * nv, dv)
+        y = gated_rmsnorm(core, z[r].reshape(T * nv, dv), norm_w, eps, bf16).reshape(T, nv * dv)
+        ys.append(y)
+        tails.append(tail)
+        states.append(s)
+    return np.stack(ys), np.stack(tails), np.stack(states)

@@ -10,7 +10,13 @@
  *   inv_unit_lower             qwen35.rs:256-296 (recursive block inversion)
  *   chunk_gated_delta_rule     qwen35.rs:298-368
  *   depthwise conv + conv tail qwen35.rs:419-431, decoder.rs:137-151
+ *   gated RMSNorm . SiLU(z)    qwen35.rs:443-449
  *   the token recurrence used by the reference's own check, qwen35.rs:776-822
+ *
+ * Parity unpinned (no offline reference test covers them): the bf16
+ * rounding points of the conv (each product and partial sum, then candle's
+ * bf16 SiLU as v / (1 + exp(-v)) with each op rounded) and of the gated
+ * norm's final cast; they follow candle's per-op bf16 arithmetic.
  */
 #include <math.h>
 #include <stdint.h>
@@ -282,8 +288,8 @@ void orc_gdn_recurrence(const float* qn, const float* kn, const float* v, const 
  *   x (c, t) channel-major; tail (c, kw-1) or NULL (zeros); w (c, kw).
  *   y[c][i] = silu( sum_{u<kw} full[c][i+u] * w[c][u] ), full = [tail || x]
  *   new_tail = last kw-1 columns of full.
- * bf16 != 0 rounds each product and partial sum to bf16 (model dtype ops);
- * SiLU is evaluated in f32 and rounded once. */
+ * bf16 != 0 rounds each product and partial sum to bf16 (model dtype ops)
+ * and evaluates SiLU as bf16 ops. */
 void orc_conv_silu(const float* x, const float* tail, const float* w, int c, int t, int kw, int bf16, float* y, float* new_tail) {
   int L = t + kw - 1;
   float* full = (float*)malloc(sizeof(float) * (size_t)L);
@@ -298,10 +304,37 @@ void orc_conv_silu(const float* x, const float* tail, const float* w, int c, int
         acc = u == 0 ? term : acc + term;
         if (bf16) acc = bf16r_ext(acc);
       }
-      float sv = acc / (1.0f + expf(-acc));
-      y[(int64_t)ch * t + i] = bf16 ? bf16r_ext(sv) : sv;
+      float sv;
+      if (bf16) {
+        /* candle's bf16 SiLU: v / (1 + exp(-v)), each op in bf16 */
+        float e = bf16r_ext(expf(-acc));
+        float den = bf16r_ext(1.0f + e);
+        sv = bf16r_ext(acc / den);
+      } else {
+        sv = acc / (1.0f + expf(-acc));
+      }
+      y[(int64_t)ch * t + i] = sv;
     }
     for (int i = 0; i < kw - 1; ++i) new_tail[(int64_t)ch * (kw - 1) + i] = full[t + i];
   }
   free(full);
+}
+
+/* Gated RMSNorm per head (qwen35.rs:443-449), f32 like the reference:
+ *   y = core / sqrt(mean(core^2) + eps) * w * silu(z),  silu(z) = z / (1 + e^-z)
+ * core, z: (rows, dv) f32 (z already cast from the model dtype); w: (dv).
+ * bf16 != 0 rounds y to bf16 (the final .to_dtype(x.dtype())). */
+void orc_gated_rmsnorm(const float* core, const float* z, const float* w, int64_t rows, int dv, float eps, int bf16, float* y) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* c = core + r * dv;
+    float s = 0.0f;
+    for (int i = 0; i < dv; ++i) s += c[i] * c[i];
+    float den = sqrtf(s / (float)dv + eps);
+    for (int i = 0; i < dv; ++i) {
+      float zz = z[r * dv + i];
+      float g = zz / (1.0f + expf(-zz));
+      float v = c[i] / den * w[i] * g;
+      y[r * dv + i] = bf16 ? bf16r_ext(v) : v;
+    }
+  }
 }

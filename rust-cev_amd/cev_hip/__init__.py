@@ -17,9 +17,10 @@ from typing import Optional, Sequence
 import numpy as np
 
 from . import synth  # noqa: F401  (re-exported)
-from ._abi import (CEV_BF16, CEV_F32, CEV_MAX_SPANS, AttnDesc, Block, CevError, QkNormDesc, Span, check, lib)
+from ._abi import (CEV_BF16, CEV_F32, CEV_MAX_SPANS, AttnDesc, Block, CevError, GdnDesc, QkNormDesc, Span, check, lib)
 
 __all__ = [
+    "GatedDeltaNet",
     "CEV_BF16", "CEV_F32", "CevError", "Block", "Span", "BlockTable", "AttnPlan", "PackedAttention",
     "packed_attention", "qknorm_rope", "rope_table", "Rotary", "device_info", "synth",
 ]
@@ -330,3 +331,68 @@ def device_info(device: int = 0) -> DeviceInfo:
     cus, hbm, clk = C.c_int32(), C.c_int64(), C.c_int32()
     check(lib().cev_device_info(device, name, 128, C.byref(cus), C.byref(hbm), C.byref(clk)))
     return DeviceInfo(name.value.decode(), cus.value, hbm.value, clk.value)
+
+
+# ---------------------------------------------------------------------------
+# Gated DeltaNet layer core
+
+
+class GatedDeltaNet:
+    """The part of GatedDeltaNet::forward (qwen35.rs:414-453) between the input
+    projections and out_proj, on the device: conv + SiLU with its state,
+    l2norm / sigmoid / softplus gates, chunk_gated_delta_rule and the gated
+    RMSNorm.  The projections stay the caller's GEMMs.
+
+    Tensors: mixed (B, T, 2 nk dk + nv dv), z (B, T, nv dv), b, a (B, T, nv)
+    and conv_w (conv_dim, K) in the model dtype; neg_a = -exp(A_log), dt_bias
+    and norm_w f32; conv_in (B, conv_dim, K-1) in the model dtype and s_in
+    (B, nv, dk, dv) f32, either may have batch stride 0 (one state for every
+    row) or be None (zero state).  Returns (y (B, T, nv dv), conv_out, s_out)."""
+
+    def __init__(self, batch: int, t: int, n_k_heads: int, n_v_heads: int, head_k_dim: int = 128, head_v_dim: int = 128,
+                 conv_kernel: int = 4, eps: float = 1e-6, dtype=None, device=None):
+        torch = _torch()
+        dtype = torch.bfloat16 if dtype is None else dtype
+        self.dtype, self.device = dtype, device
+        self.desc = GdnDesc()
+        code = CEV_BF16 if dtype == torch.bfloat16 else CEV_F32
+        check(lib().cev_gdn_desc_init(C.byref(self.desc), code, batch, t, n_k_heads, n_v_heads, head_k_dim, head_v_dim,
+                                      conv_kernel, float(eps)))
+        n = C.c_size_t(0)
+        check(lib().cev_gdn_workspace_size(C.byref(self.desc), C.byref(n)))
+        self.workspace = torch.empty(n.value, dtype=torch.uint8, device=device)
+        self.conv_dim = 2 * n_k_heads * head_k_dim + n_v_heads * head_v_dim
+        self.shape = (batch, t, n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_kernel)
+
+    def __call__(self, mixed, z, b, a, conv_w, neg_a, dt_bias, norm_w, conv_in=None, s_in=None, y=None, conv_out=None,
+                 s_out=None, stream=None):
+        torch = _torch()
+        B, T, nk, nv, dk, dv, K = self.shape
+        D = self.desc
+        for name, x in (("mixed", mixed), ("z", z), ("b", b), ("a", a)):
+            if x.stride(-1) != 1 or x.dtype != self.dtype:
+                raise ValueError(f"{name} must be {self.dtype} with unit channel stride")
+        D.mixed_stride_b, D.mixed_stride_t = mixed.stride(0), mixed.stride(1)
+        D.z_stride_b, D.z_stride_t = z.stride(0), z.stride(1)
+        if a.stride() != b.stride():
+            raise ValueError("a and b must share strides")
+        D.ab_stride_b, D.ab_stride_t = a.stride(0), a.stride(1)
+        if conv_in is not None:
+            if conv_in.stride(1) != K - 1 or conv_in.stride(2) != 1:
+                raise ValueError("conv_in must be (B, conv_dim, K-1) with contiguous rows")
+            D.conv_in_stride_b = conv_in.stride(0)
+        if s_in is not None:
+            if s_in.dtype != torch.float32 or tuple(s_in.stride()[1:]) != (dk * dv, dv, 1):
+                raise ValueError("s_in must be f32 (B, nv, dk, dv) with contiguous heads")
+            D.s_in_stride_b = s_in.stride(0)
+        if y is None:
+            y = torch.empty((B, T, nv * dv), dtype=self.dtype, device=mixed.device)
+        D.y_stride_b, D.y_stride_t = y.stride(0), y.stride(1)
+        if conv_out is None:
+            conv_out = torch.empty((B, self.conv_dim, K - 1), dtype=self.dtype, device=mixed.device)
+        if s_out is None:
+            s_out = torch.empty((B, nv, dk, dv), dtype=torch.float32, device=mixed.device)
+        check(lib().cev_gdn_forward(C.byref(D), _ptr(mixed), _ptr(z), _ptr(b), _ptr(a), _ptr(conv_w), _ptr(neg_a), _ptr(dt_bias),
+                                    _ptr(norm_w), _ptr(conv_in), _ptr(s_in), _ptr(y), _ptr(conv_out), _ptr(s_out),
+                                    _ptr(self.workspace), self.workspace.numel(), _stream_ptr(stream)))
+        return y, conv_out, s_out

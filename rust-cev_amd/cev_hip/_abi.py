@@ -72,6 +72,18 @@ class QkNormDesc(C.Structure):
     ]
 
 
+class GdnDesc(C.Structure):
+    _fields_ = [
+        ("dtype", i32), ("batch", i32), ("t", i32), ("n_k_heads", i32), ("n_v_heads", i32),
+        ("head_k_dim", i32), ("head_v_dim", i32), ("conv_kernel", i32), ("eps", C.c_float), ("reserved", i32),
+        ("mixed_stride_b", i64), ("mixed_stride_t", i64),
+        ("z_stride_b", i64), ("z_stride_t", i64),
+        ("ab_stride_b", i64), ("ab_stride_t", i64),
+        ("conv_in_stride_b", i64), ("s_in_stride_b", i64),
+        ("y_stride_b", i64), ("y_stride_t", i64),
+    ]
+
+
 P = C.c_void_p
 Pi32 = C.POINTER(i32)
 PBlock = C.POINTER(Block)
@@ -86,6 +98,9 @@ SIGNATURES = {
     "cev_qknorm_desc_init": (i32, [C.POINTER(QkNormDesc), i32, i32, i32, i32, i32, i32, i32, i32, C.c_float, i32]),
     "cev_qknorm_rope": (i32, [C.POINTER(QkNormDesc), P, P, P, P, P, P, P, P, P, P]),
     "cev_rope_table": (i32, [C.c_double, i32, i32, i32, P, P]),
+    "cev_gdn_desc_init": (i32, [C.POINTER(GdnDesc), i32, i32, i32, i32, i32, i32, i32, i32, C.c_float]),
+    "cev_gdn_workspace_size": (i32, [C.POINTER(GdnDesc), C.POINTER(C.c_size_t)]),
+    "cev_gdn_forward": (i32, [C.POINTER(GdnDesc), P, P, P, P, P, P, P, P, P, P, P, P, P, P, C.c_size_t, P]),
     "cev_table_from_plans": (i32, [i32, Pi32, Pi32, Pi32, i32, Pi32, Pi32, PBlock, i32, Pi32, Pi32, i32, Pi32, Pi32]),
     "cev_table_from_rows": (i32, [i32, i32, i32, i32, Pi32, PBlock, i32]),
     "cev_table_from_segment_ids": (i32, [C.POINTER(C.c_uint32), i32, i32, PBlock, i32, Pi32]),

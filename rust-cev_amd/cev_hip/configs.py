@@ -150,3 +150,55 @@ def c5_attention() -> AttnWorkload:
 
 
 WORKLOADS = {"c1": c1, "c3": c3, "c4": c4, "c5a": c5_attention, "hbm": hbm}
+
+
+@dataclass
+class GdnWorkload:
+    """One Gated DeltaNet layer of a Qwen3.5 hybrid prefix (config 5's GDN
+    part: Hk = 16 repeated to Hv = 32, dk = dv = 128, conv kernel 4, 64-token
+    chunks).  Synthetic inputs stand for the projection outputs: q/k/v/z
+    N(0,1); beta = sigmoid(b) uniform in (0, 1) and the per-token decay
+    e^g log-uniform in [1e-3, 1] (b = logit(u), a = softplus^-1(-g) with
+    dt_bias = 0, -e^A = -1)."""
+    name: str
+    seed: int
+    bf16: bool
+    batch: int
+    t: int
+    nk: int = 16
+    nv: int = 32
+    dk: int = 128
+    dv: int = 128
+    kernel: int = 4
+    eps: float = 1e-6
+
+    @property
+    def conv_dim(self) -> int:
+        return 2 * self.nk * self.dk + self.nv * self.dv
+
+    def flops(self) -> float:
+        """chunk_gated_delta_rule multiply-adds (x2) per head and 64-token chunk:
+        k k^T, q k^T, inv v, inv k, k_cumdecay S, q S, intra v_new, k^T v_new."""
+        n = -(-self.t // 64)
+        per = 2 * (64 * 64 * self.dk * 2 + 64 * 64 * (self.dv + self.dk) + 64 * self.dk * self.dv * 3 + 64 * 64 * self.dv)
+        return float(per) * n * self.nv * self.batch
+
+    def inputs(self):
+        from .synth import round_bf16, tensor, uniform
+        B, T, s = self.batch, self.t, self.seed
+        rb = round_bf16 if self.bf16 else (lambda x: x)
+        mixed = tensor(s, 1, (B, T, self.conv_dim), self.bf16)
+        z = tensor(s, 2, (B, T, self.nv * self.dv), self.bf16)
+        u = np.clip(uniform(s, 3, B * T * self.nv), 1e-4, 1 - 1e-4).reshape(B, T, self.nv)
+        b = rb(np.log(u / (1.0 - u)).astype(np.float32))
+        g = (np.log(1e-3) * uniform(s, 4, B * T * self.nv)).reshape(B, T, self.nv)
+        a = rb(np.log(np.expm1(np.maximum(-g, 1e-6))).astype(np.float32))
+        conv_w = tensor(s, 5, (self.conv_dim, self.kernel), self.bf16, scale=0.5)
+        neg_a = -np.ones(self.nv, np.float32)
+        dt_bias = np.zeros(self.nv, np.float32)
+        norm_w = (1.0 + 0.1 * tensor(s, 6, (self.dv,), False)).astype(np.float32)
+        return dict(mixed=mixed, z=z, b=b, a=a, conv_w=conv_w, neg_a=neg_a, dt_bias=dt_bias, norm_w=norm_w)
+
+
+def c5_gdn(t: int = 4096, batch: int = 1) -> GdnWorkload:
+    return GdnWorkload(f"c5gdn{batch}x{t}", 5, True, batch, t)

@@ -1,0 +1,632 @@
+// Gated DeltaNet layer core for gfx950: the replacement for the part of
+// GatedDeltaNet::forward (crates/cev-model/src/qwen35.rs:414-453) between the
+// input projections and out_proj.
+//
+//   conv:  depthwise causal conv over [conv state || x] + SiLU, new state
+//          (qwen35.rs:424-428, decoder.rs:137-151), model dtype ops;
+//   prep:  per (row, value head, 64-token chunk), in f32: q, k l2norm
+//          (q * dk^-0.5), beta = sigmoid(b), g = softplus(a + dt_bias) * -e^A,
+//          cum = prefix sum of g, ut = (k beta) k^T * pair, intra = q k^T * pair,
+//          inv = (I + strict_lower(ut))^-1, new_values = inv (v beta),
+//          k_cumdecay = inv (k beta e^cum) (qwen35.rs:301-345);
+//   scan:  the sequential chunk recurrence (qwen35.rs:346-365) with the
+//          state split into 16-column slices (columns of S evolve
+//          independently), one workgroup per (row, head, slice);
+//   norm:  gated RMSNorm * SiLU(z) and the cast to the model dtype
+//          (qwen35.rs:443-449).
+//
+// All chunk-rule products run on v_mfma_f32_16x16x4_f32 (full f32 like the
+// reference).  Lane layout (16x16x4): A lane l holds A[l%16][l/16], B lane l
+// holds B[l/16][l%16], D lane l register r holds D[4(l/16)+r][l%16].
+#include <cstring>
+
+#include "cev_device.h"
+#include "cev_internal.h"
+
+namespace {
+
+constexpr int kC = 64;     // chunk length (qwen35.rs:302)
+constexpr int kD = 128;    // head_k_dim = head_v_dim supported here
+constexpr int kW = 16;     // state columns per scan workgroup
+constexpr int kSX = 132;   // LDS row stride (floats) of 128-wide f32 tiles
+constexpr int kSC = 68;    // LDS row stride of 64-wide f32 tiles
+// Per (row, head, chunk) record in the workspace, in floats.
+constexpr int kRecQd = 0;                    // q * e^cum          (64 x 128)
+constexpr int kRecKd = kRecQd + kC * kD;     // k * e^(last - cum) (64 x 128)
+constexpr int kRecKcd = kRecKd + kC * kD;    // k_cumdecay         (64 x 128)
+constexpr int kRecNv = kRecKcd + kC * kD;    // new_values         (64 x 128)
+constexpr int kRecIntra = kRecNv + kC * kD;  // intra              (64 x 64)
+constexpr int kRecDecay = kRecIntra + kC * kC;
+constexpr int kRecFloats = kRecDecay + 16;
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4v mma16(float a, float b, f32x4v c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+template <typename T>
+__device__ __forceinline__ float to_f(T x) {
+  return (float)x;
+}
+template <typename T>
+__device__ __forceinline__ T from_f(float x);
+template <>
+__device__ __forceinline__ float from_f<float>(float x) {
+  return x;
+}
+template <>
+__device__ __forceinline__ __bf16 from_f<__bf16>(float x) {
+  return (__bf16)x;
+}
+template <typename T>
+__device__ __forceinline__ float rnd(float x) {  // one model-dtype op result
+  return sizeof(T) == 2 ? bf16_round(x) : x;
+}
+
+struct GdnArgs {
+  const void* mixed;
+  const void* z;
+  const void* b;
+  const void* a;
+  const void* conv_w;
+  const float* neg_a;
+  const float* dt_bias;
+  const float* norm_w;
+  const void* conv_in;
+  const float* s_in;
+  void* y;
+  void* conv_out;
+  float* s_out;
+  void* conved;  // workspace: (B, T, conv_dim) model dtype
+  float* rec;    // workspace: (B, nv, n_chunks) records
+  float* core;   // workspace: (B, T, nv, dv) f32
+  int64_t mixed_sb, mixed_st, z_sb, z_st, ab_sb, ab_st, conv_in_sb, s_in_sb, y_sb, y_st;
+  int32_t batch, t, nk, nv, kernel, conv_dim, n_chunks;
+  float eps;
+};
+
+// ---------------------------------------------------------------------------
+// conv + SiLU.  Thread = (row, token, 8 channels).  Each product and partial
+// sum is one model-dtype op (decoder.rs:143-150); SiLU is candle's
+// v / (1 + exp(-v)) with each op in the model dtype.
+template <typename T>
+__global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs g) {
+  const int64_t cg = g.conv_dim / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)g.batch * g.t * cg) return;
+  const int c0 = (int)(idx % cg) * 8;
+  const int64_t rt = idx / cg;
+  const int t = (int)(rt % g.t), r = (int)(rt / g.t);
+  const T* x = (const T*)g.mixed + r * g.mixed_sb;
+  const T* tail = g.conv_in ? (const T*)g.conv_in + r * g.conv_in_sb : nullptr;
+  const T* w = (const T*)g.conv_w;
+  const int K = g.kernel;
+  float acc[8];
+  for (int u = 0; u < K; ++u) {
+    const int p = t + u - (K - 1);  // source token; < 0 reads the conv state
+    float xv[8];
+    if (p >= 0) {
+      const T* xp = x + p * g.mixed_st + c0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[e] = to_f(xp[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[e] = tail ? to_f(tail[(int64_t)(c0 + e) * (K - 1) + (K - 1 + p)]) : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float term = rnd<T>(xv[e] * to_f(w[(int64_t)(c0 + e) * K + u]));
+      acc[e] = u == 0 ? term : rnd<T>(acc[e] + term);
+    }
+  }
+  T* out = (T*)g.conved + ((int64_t)r * g.t + t) * g.conv_dim + c0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = acc[e];
+    float s;
+    if (sizeof(T) == 2) {
+      const float ex = bf16_round(expf(-v));
+      const float den = bf16_round(1.0f + ex);
+      s = bf16_round(v / den);
+    } else {
+      s = v / (1.0f + expf(-v));
+    }
+    out[e] = from_f<T>(s);
+  }
+}
+
+// New conv state: the last K-1 columns of [state || x] (qwen35.rs:425).
+template <typename T>
+__global__ __launch_bounds__(256) void gdn_conv_state_kernel(GdnArgs g) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)g.batch * g.conv_dim) return;
+  const int c = (int)(idx % g.conv_dim), r = (int)(idx / g.conv_dim);
+  const int K = g.kernel;
+  const T* x = (const T*)g.mixed + r * g.mixed_sb;
+  const T* tail = g.conv_in ? (const T*)g.conv_in + r * g.conv_in_sb : nullptr;
+  T* out = (T*)g.conv_out + ((int64_t)r * g.conv_dim + c) * (K - 1);
+  for (int i = 0; i < K - 1; ++i) {
+    const int f = g.t + i;  // index into [state || x]
+    T v;
+    if (f < K - 1)
+      v = tail ? tail[(int64_t)c * (K - 1) + f] : from_f<T>(0.0f);
+    else
+      v = x[(int64_t)(f - (K - 1)) * g.mixed_st + c];
+    out[i] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// prep: one workgroup (4 waves) per (row, value head, chunk).
+template <typename T>
+__global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
+  __shared__ float Qs[kC * kSX];
+  __shared__ float Ks[kC * kSX];
+  __shared__ float Vs[kC * kSX];
+  __shared__ float Us[kC * kSC];   // strict lower ut
+  __shared__ float Iv[kC * kSC];   // (I + Us)^-1
+  __shared__ float Tm[kC * kSC];   // products of the block inversion
+  __shared__ float gs[kC], betas[kC], cums[kC];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = blockIdx.x % g.n_chunks;
+  const int hr = blockIdx.x / g.n_chunks;
+  const int h = hr % g.nv, r = hr / g.nv;
+  const int kh = h / (g.nv / g.nk);  // value head h reads key head h / (nv/nk) (qwen35.rs:433-437)
+  const int key_dim = g.nk * kD;
+  const int t0 = c * kC;
+
+  // ---- load q, k, v of the chunk (rows past t are the zero padding)
+  const T* cv = (const T*)g.conved + (int64_t)r * g.t * g.conv_dim;
+  for (int p = tid; p < kC * (kD / 8); p += 256) {
+    const int i = p / (kD / 8), col = (p % (kD / 8)) * 8;
+    const int t = t0 + i;
+    float qv[8], kv[8], vv[8];
+    if (t < g.t) {
+      const T* row = cv + (int64_t)t * g.conv_dim;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qv[e] = to_f(row[kh * kD + col + e]);
+        kv[e] = to_f(row[key_dim + kh * kD + col + e]);
+        vv[e] = to_f(row[2 * key_dim + h * kD + col + e]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[e] = kv[e] = vv[e] = 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      Qs[i * kSX + col + e] = qv[e];
+      Ks[i * kSX + col + e] = kv[e];
+      Vs[i * kSX + col + e] = vv[e];
+    }
+  }
+  if (tid < kC) {
+    const int t = t0 + tid;
+    float gv = 0.0f, bv = 0.0f;
+    if (t < g.t) {
+      const float av = to_f(((const T*)g.a)[r * g.ab_sb + (int64_t)t * g.ab_st + h]);
+      const float bb = to_f(((const T*)g.b)[r * g.ab_sb + (int64_t)t * g.ab_st + h]);
+      const float x = av + g.dt_bias[h];
+      const float sp = fmaxf(x, 0.0f) + logf(expf(-fabsf(x)) + 1.0f);  // softplus (qwen35.rs:243-248)
+      gv = sp * g.neg_a[h];
+      bv = 1.0f / (1.0f + expf(-bb));
+    }
+    gs[tid] = gv;
+    betas[tid] = bv;
+  }
+  __syncthreads();
+
+  // ---- l2norm of q (then * dk^-0.5) and k rows: wave w takes rows w, w+4, ...
+  const float qscale = 0.08838834764831845f;  // 128^-0.5
+  for (int i = wave; i < 2 * kC; i += 4) {
+    float* row = i < kC ? Qs + i * kSX : Ks + (i - kC) * kSX;
+    const float x0 = row[lane], x1 = row[lane + 64];
+    float s = x0 * x0 + x1 * x1;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    const float n = sqrtf(s + 1e-6f);
+    const float sc = i < kC ? qscale : 1.0f;
+    row[lane] = x0 / n * sc;
+    row[lane + 64] = x1 / n * sc;
+  }
+  if (tid == 0) {
+    float acc = 0.0f;
+    for (int i = 0; i < kC; ++i) {
+      acc += gs[i];
+      cums[i] = acc;
+    }
+  }
+  __syncthreads();
+
+  float* rec = g.rec + (int64_t)blockIdx.x * kRecFloats;
+  const int fm = lane & 15, fq = lane >> 4;  // fragment row / k-slot of this lane
+
+  // ---- G = K K^T and QK = Q K^T on the lower 16x16 tiles; ut, intra.
+  // Tile list (ti, tj), tj <= ti, dealt round-robin to the waves.
+  for (int tile = wave; tile < 16; tile += 4) {
+    const int ti = tile / 4, tj = tile % 4;
+    f32x4v gacc = {0, 0, 0, 0}, qacc = {0, 0, 0, 0};
+    if (tj <= ti) {
+      for (int k = 0; k < kD; k += 4) {
+        const float bk = Ks[(16 * tj + fm) * kSX + k + fq];
+        gacc = mma16(Ks[(16 * ti + fm) * kSX + k + fq], bk, gacc);
+        qacc = mma16(Qs[(16 * ti + fm) * kSX + k + fq], bk, qacc);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * ti + 4 * fq + e, j = 16 * tj + fm;
+      const float pair = j <= i ? expf(cums[i] - cums[j]) : 0.0f;
+      Us[i * kSC + j] = j < i ? betas[i] * gacc[e] * pair : 0.0f;
+      rec[kRecIntra + i * kC + j] = qacc[e] * pair;
+    }
+  }
+  __syncthreads();
+
+  // ---- inv = (I + L)^-1, L = Us strict lower, by the block recursion of
+  // inv_unit_lower (qwen35.rs:277-296) over 16, 32, 64:
+  //   [A 0; C B]^-1 = [A^-1 0; -(B^-1 C) A^-1  B^-1].
+  // 16x16 diagonal blocks by forward substitution (wave w, block w).
+  {
+    const int b0 = 16 * wave;
+    const int j = lane & 15;
+    if (lane < 16) {
+      for (int i = 0; i < 16; ++i) Iv[(b0 + i) * kSC + b0 + j] = i == j ? 1.0f : 0.0f;
+    }
+    for (int i = 1; i < 16; ++i) {
+      // row i = -sum_{k<i} L[i][k] inv[k][:]
+      if (lane < 16 && j < i) {
+        float s = 0.0f;
+        for (int k = j; k < i; ++k) s += Us[(b0 + i) * kSC + b0 + k] * Iv[(b0 + k) * kSC + b0 + j];
+        Iv[(b0 + i) * kSC + b0 + j] = -s;
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
+  }
+  __syncthreads();
+  // 32x32 level: blocks [0,32) (wave 0) and [32,64) (wave 1): off-diagonal
+  // 16x16 block = -(B^-1 C) A^-1.
+  if (wave < 2) {
+    const int o = 32 * wave;  // block origin
+    const float* Ainv = Iv + o * kSC + o;                  // rows o..o+15, cols o..o+15
+    const float* Binv = Iv + (o + 16) * kSC + o + 16;      // rows o+16.., cols o+16..
+    const float* Cb = Us + (o + 16) * kSC + o;             // rows o+16.., cols o..
+    f32x4v bc = {0, 0, 0, 0};
+    for (int k = 0; k < 16; k += 4) bc = mma16(Binv[fm * kSC + k + fq], Cb[(k + fq) * kSC + fm], bc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Tm[(o + 4 * fq + e) * kSC + fm] = bc[e];  // B^-1 C, rows 0..15 of the block
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    f32x4v x = {0, 0, 0, 0};
+    for (int k = 0; k < 16; k += 4) x = mma16(Tm[(o + fm) * kSC + k + fq], Ainv[(k + fq) * kSC + fm], x);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Iv[(o + 16 + 4 * fq + e) * kSC + o + fm] = -x[e];
+    // the upper off-diagonal block stays zero
+    for (int e = 0; e < 4; ++e) Iv[(o + 4 * fq + e) * kSC + o + 16 + fm] = 0.0f;
+  }
+  __syncthreads();
+  // 64x64 level: off block (rows 32..63, cols 0..31) = -(B^-1 C) A^-1 with
+  // 32x32 A^-1 = Iv[0:32,0:32], B^-1 = Iv[32:64,32:64], C = Us[32:64,0:32].
+  // Wave w computes the 16x16 tile (w/2, w%2) of B^-1 C, then of the product.
+  {
+    const int ti = wave >> 1, tj = wave & 1;
+    f32x4v bc = {0, 0, 0, 0};
+    for (int k = 0; k < 32; k += 4)
+      bc = mma16(Iv[(32 + 16 * ti + fm) * kSC + 32 + k + fq], Us[(32 + k + fq) * kSC + 16 * tj + fm], bc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Tm[(16 * ti + 4 * fq + e) * kSC + 16 * tj + fm] = bc[e];
+  }
+  __syncthreads();
+  {
+    const int ti = wave >> 1, tj = wave & 1;
+    f32x4v x = {0, 0, 0, 0};
+    for (int k = 0; k < 32; k += 4) x = mma16(Tm[(16 * ti + fm) * kSC + k + fq], Iv[(k + fq) * kSC + 16 * tj + fm], x);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Iv[(32 + 16 * ti + 4 * fq + e) * kSC + 16 * tj + fm] = -x[e];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Iv[(16 * ti + 4 * fq + e) * kSC + 32 + 16 * tj + fm] = 0.0f;
+  }
+  __syncthreads();
+
+  // ---- new_values = inv (v beta), k_cumdecay = inv (k beta e^cum):
+  // 4 x 8 output tiles each; the K range of row tile ti stops at its
+  // diagonal block (inv is lower triangular).
+  for (int tile = wave; tile < 32; tile += 4) {
+    const int ti = tile / 8, tn = tile % 8;
+    f32x4v nv = {0, 0, 0, 0}, kc = {0, 0, 0, 0};
+    for (int k = 0; k < 16 * (ti + 1); k += 4) {
+      const float av = Iv[(16 * ti + fm) * kSC + k + fq];
+      const int kk = k + fq;
+      const float bsc = betas[kk];
+      nv = mma16(av, Vs[kk * kSX + 16 * tn + fm] * bsc, nv);
+      kc = mma16(av, Ks[kk * kSX + 16 * tn + fm] * bsc * expf(cums[kk]), kc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * ti + 4 * fq + e, col = 16 * tn + fm;
+      rec[kRecNv + i * kD + col] = nv[e];
+      rec[kRecKcd + i * kD + col] = kc[e];
+    }
+  }
+  // ---- q e^cum, k e^(last - cum), e^last
+  const float last = cums[kC - 1];
+  for (int p = tid; p < kC * kD; p += 256) {
+    const int i = p / kD, col = p % kD;
+    rec[kRecQd + p] = Qs[i * kSX + col] * expf(cums[i]);
+    rec[kRecKd + p] = Ks[i * kSX + col] * expf(last - cums[i]);
+  }
+  if (tid == 0) rec[kRecDecay] = expf(last);
+}
+
+// ---------------------------------------------------------------------------
+// scan: one workgroup (4 waves) per (row, value head, 16-column slice of the
+// state).  Per chunk (qwen35.rs:353-364):
+//   v_new = new_values - k_cumdecay . S;   out = (q e^cum) . S + intra . v_new;
+//   S = S e^last + (k e^(last-cum))^T . v_new.
+__global__ __launch_bounds__(256) void gdn_scan_kernel(GdnArgs g) {
+  __shared__ float Kc[kC * kSX];   // k_cumdecay
+  __shared__ float Qd[kC * kSX];   // q e^cum
+  __shared__ float Kd[kC * kSX];   // k e^(last - cum)
+  __shared__ float In[kC * kSC];   // intra
+  __shared__ float Nv[kC * 20];    // new_values, this slice
+  __shared__ float Vn[kC * 20];    // v_new
+  __shared__ float S[kD * 20];     // state slice (dk x 16)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nslice = kD / kW;
+  const int sl = blockIdx.x % nslice;
+  const int hr = blockIdx.x / nslice;
+  const int h = hr % g.nv, r = hr / g.nv;
+  const int col0 = sl * kW;
+  const int fm = lane & 15, fq = lane >> 4;
+
+  for (int p = tid; p < kD * kW; p += 256) {
+    const int i = p / kW, j = p % kW;
+    S[i * 20 + j] = g.s_in ? g.s_in[r * g.s_in_sb + ((int64_t)h * kD + i) * kD + col0 + j] : 0.0f;
+  }
+  for (int c = 0; c < g.n_chunks; ++c) {
+    const float* rec = g.rec + ((int64_t)hr * g.n_chunks + c) * kRecFloats;
+    for (int p = tid; p < kC * kD / 4; p += 256) {
+      const int i = p / (kD / 4), col = (p % (kD / 4)) * 4;
+      const f32x4 q = *(const f32x4*)(rec + kRecQd + i * kD + col);
+      const f32x4 kd = *(const f32x4*)(rec + kRecKd + i * kD + col);
+      const f32x4 kc = *(const f32x4*)(rec + kRecKcd + i * kD + col);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        Qd[i * kSX + col + e] = q[e];
+        Kd[i * kSX + col + e] = kd[e];
+        Kc[i * kSX + col + e] = kc[e];
+      }
+    }
+    for (int p = tid; p < kC * kC / 4; p += 256) {
+      const int i = p / (kC / 4), col = (p % (kC / 4)) * 4;
+      const f32x4 v = *(const f32x4*)(rec + kRecIntra + i * kC + col);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) In[i * kSC + col + e] = v[e];
+    }
+    for (int p = tid; p < kC * kW; p += 256) {
+      const int i = p / kW, j = p % kW;
+      Nv[i * 20 + j] = rec[kRecNv + i * kD + col0 + j];
+    }
+    const float decay = rec[kRecDecay];
+    __syncthreads();
+
+    // phase 1: wave w owns rows 16w..16w+15 of v_new and of out
+    f32x4v kS = {0, 0, 0, 0}, qS = {0, 0, 0, 0};
+    for (int k = 0; k < kD; k += 4) {
+      const float b = S[(k + fq) * 20 + fm];
+      kS = mma16(Kc[(16 * wave + fm) * kSX + k + fq], b, kS);
+      qS = mma16(Qd[(16 * wave + fm) * kSX + k + fq], b, qS);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * wave + 4 * fq + e;
+      Vn[i * 20 + fm] = Nv[i * 20 + fm] - kS[e];
+    }
+    __syncthreads();
+    // phase 2: out rows of wave w; S rows 32w..32w+31
+    for (int k = 0; k < 16 * (wave + 1); k += 4) qS = mma16(In[(16 * wave + fm) * kSC + k + fq], Vn[(k + fq) * 20 + fm], qS);
+    f32x4v s0 = {0, 0, 0, 0}, s1 = {0, 0, 0, 0};
+    for (int k = 0; k < kC; k += 4) {
+      const float b = Vn[(k + fq) * 20 + fm];
+      s0 = mma16(Kd[(k + fq) * kSX + 32 * wave + fm], b, s0);
+      s1 = mma16(Kd[(k + fq) * kSX + 32 * wave + 16 + fm], b, s1);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * wave + 4 * fq + e;
+      const int t = c * kC + i;
+      if (t < g.t) g.core[(((int64_t)r * g.t + t) * g.nv + h) * kD + col0 + fm] = qS[e];
+      const int r0 = 32 * wave + 4 * fq + e;
+      S[r0 * 20 + fm] = S[r0 * 20 + fm] * decay + s0[e];
+      S[(r0 + 16) * 20 + fm] = S[(r0 + 16) * 20 + fm] * decay + s1[e];
+    }
+    __syncthreads();
+  }
+  for (int p = tid; p < kD * kW; p += 256) {
+    const int i = p / kW, j = p % kW;
+    g.s_out[((int64_t)r * g.nv + h) * kD * kD + (int64_t)i * kD + col0 + j] = S[i * 20 + j];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// norm: one wave per (row, token, value head): y = core / sqrt(mean core^2
+// + eps) * w * silu(z), cast to the model dtype (qwen35.rs:443-449).
+template <typename T>
+__global__ __launch_bounds__(256) void gdn_norm_kernel(GdnArgs g) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= (int64_t)g.batch * g.t * g.nv) return;
+  const int h = (int)(item % g.nv);
+  const int64_t rt = item / g.nv;
+  const int t = (int)(rt % g.t), r = (int)(rt / g.t);
+  const float* cr = g.core + item * kD;
+  const float c0 = cr[lane], c1 = cr[lane + 64];
+  float s = c0 * c0 + c1 * c1;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float den = sqrtf(s / (float)kD + g.eps);
+  const T* zr = (const T*)g.z + r * g.z_sb + (int64_t)t * g.z_st + h * kD;
+  T* yr = (T*)g.y + r * g.y_sb + (int64_t)t * g.y_st + h * kD;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int i = lane + 64 * e;
+    const float zz = to_f(zr[i]);
+    const float gate = zz / (1.0f + expf(-zz));
+    yr[i] = from_f<T>((e ? c1 : c0) / den * g.norm_w[i] * gate);
+  }
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct GdnLayout {
+  size_t conved, rec, core, total;
+};
+
+GdnLayout gdn_layout(const cev_gdn_desc* d) {
+  const size_t esz = d->dtype == CEV_BF16 ? 2 : 4;
+  const int64_t conv_dim = 2LL * d->n_k_heads * d->head_k_dim + (int64_t)d->n_v_heads * d->head_v_dim;
+  const int64_t n_chunks = (d->t + kC - 1) / kC;
+  GdnLayout L;
+  L.conved = 0;
+  L.rec = align256((size_t)d->batch * d->t * conv_dim * esz);
+  L.core = L.rec + align256((size_t)d->batch * d->n_v_heads * n_chunks * kRecFloats * sizeof(float));
+  L.total = L.core + align256((size_t)d->batch * d->t * d->n_v_heads * d->head_v_dim * sizeof(float));
+  return L;
+}
+
+int32_t check_gdn(const cev_gdn_desc* d) {
+  CEV_CHECK_ARG(d != nullptr, "null GDN descriptor");
+  if (d->dtype != CEV_F32 && d->dtype != CEV_BF16) return cev_fail(CEV_ERR_UNSUPPORTED, "dtype %d not supported", d->dtype);
+  CEV_CHECK_ARG(d->batch >= 1 && d->t >= 1, "batch %d and t %d must be positive", d->batch, d->t);
+  CEV_CHECK_ARG(d->n_k_heads >= 1 && d->n_v_heads >= 1 && d->n_v_heads % d->n_k_heads == 0,
+                "n_v_heads %d must be a positive multiple of n_k_heads %d", d->n_v_heads, d->n_k_heads);
+  if (d->head_k_dim != kD || d->head_v_dim != kD)
+    return cev_fail(CEV_ERR_UNSUPPORTED, "head dims %d x %d not supported (128 x 128)", d->head_k_dim, d->head_v_dim);
+  CEV_CHECK_ARG(d->conv_kernel >= 2 && d->conv_kernel <= 8, "conv_kernel %d outside [2, 8]", d->conv_kernel);
+  CEV_CHECK_ARG(d->eps >= 0.0f && d->eps <= 3.4e38f, "eps must be finite and non-negative");
+  const int64_t* st[] = {&d->mixed_stride_b, &d->mixed_stride_t, &d->z_stride_b, &d->z_stride_t, &d->ab_stride_b,
+                         &d->ab_stride_t, &d->conv_in_stride_b, &d->s_in_stride_b, &d->y_stride_b, &d->y_stride_t};
+  for (const int64_t* s : st) CEV_CHECK_ARG(*s >= 0, "negative stride");
+  const int64_t conv_dim = 2LL * d->n_k_heads * kD + (int64_t)d->n_v_heads * kD;
+  CEV_CHECK_ARG(d->mixed_stride_t >= conv_dim && d->z_stride_t >= (int64_t)d->n_v_heads * kD && d->ab_stride_t >= d->n_v_heads &&
+                    d->y_stride_t >= (int64_t)d->n_v_heads * kD,
+                "row strides shorter than the rows");
+  return CEV_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t cev_gdn_desc_init(cev_gdn_desc* d, int32_t dtype, int32_t batch, int32_t t, int32_t n_k_heads, int32_t n_v_heads,
+                                     int32_t head_k_dim, int32_t head_v_dim, int32_t conv_kernel, float eps) {
+  CEV_CHECK_ARG(d != nullptr, "cev_gdn_desc_init: null descriptor");
+  memset(d, 0, sizeof(*d));
+  d->dtype = dtype;
+  d->batch = batch;
+  d->t = t;
+  d->n_k_heads = n_k_heads;
+  d->n_v_heads = n_v_heads;
+  d->head_k_dim = head_k_dim;
+  d->head_v_dim = head_v_dim;
+  d->conv_kernel = conv_kernel;
+  d->eps = eps;
+  const int64_t conv_dim = 2LL * n_k_heads * head_k_dim + (int64_t)n_v_heads * head_v_dim;
+  const int64_t vdim = (int64_t)n_v_heads * head_v_dim;
+  d->mixed_stride_t = conv_dim;
+  d->mixed_stride_b = conv_dim * t;
+  d->z_stride_t = vdim;
+  d->z_stride_b = vdim * t;
+  d->ab_stride_t = n_v_heads;
+  d->ab_stride_b = (int64_t)n_v_heads * t;
+  d->conv_in_stride_b = conv_dim * (conv_kernel - 1);
+  d->s_in_stride_b = (int64_t)n_v_heads * head_k_dim * head_v_dim;
+  d->y_stride_t = vdim;
+  d->y_stride_b = vdim * t;
+  return check_gdn(d);
+}
+
+extern "C" int32_t cev_gdn_workspace_size(const cev_gdn_desc* d, size_t* bytes) {
+  int32_t rc = check_gdn(d);
+  if (rc) return rc;
+  CEV_CHECK_ARG(bytes != nullptr, "cev_gdn_workspace_size: null output");
+  *bytes = gdn_layout(d).total;
+  return CEV_OK;
+}
+
+extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, const void* z, const void* b, const void* a,
+                                   const void* conv_w, const float* neg_a, const float* dt_bias, const float* norm_w,
+                                   const void* conv_in, const float* s_in, void* y, void* conv_out, float* s_out, void* workspace,
+                                   size_t workspace_bytes, cev_stream stream) {
+  int32_t rc = check_gdn(d);
+  if (rc) return rc;
+  CEV_CHECK_ARG(mixed && z && b && a && conv_w && neg_a && dt_bias && norm_w && y && conv_out && s_out,
+                "cev_gdn_forward: null input or output");
+  const GdnLayout L = gdn_layout(d);
+  CEV_CHECK_ARG(workspace != nullptr, "cev_gdn_forward: null workspace");
+  if (workspace_bytes < L.total) return cev_fail(CEV_ERR_SPACE, "workspace of %zu bytes, the layer needs %zu", workspace_bytes, L.total);
+  const size_t esz = d->dtype == CEV_BF16 ? 2 : 4;
+  const uintptr_t al = esz * 8 - 1;  // 8-element vector reads of the conv input
+  CEV_CHECK_ARG(((uintptr_t)mixed & al) == 0 && (d->mixed_stride_t % 8) == 0 && (d->mixed_stride_b % 8) == 0,
+                "cev_gdn_forward: the conv input rows must be 8-element aligned");
+  CEV_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "cev_gdn_forward: workspace must be 256-byte aligned");
+  GdnArgs g;
+  g.mixed = mixed;
+  g.z = z;
+  g.b = b;
+  g.a = a;
+  g.conv_w = conv_w;
+  g.neg_a = neg_a;
+  g.dt_bias = dt_bias;
+  g.norm_w = norm_w;
+  g.conv_in = conv_in;
+  g.s_in = s_in;
+  g.y = y;
+  g.conv_out = conv_out;
+  g.s_out = s_out;
+  g.conved = (char*)workspace + L.conved;
+  g.rec = (float*)((char*)workspace + L.rec);
+  g.core = (float*)((char*)workspace + L.core);
+  g.mixed_sb = d->mixed_stride_b;
+  g.mixed_st = d->mixed_stride_t;
+  g.z_sb = d->z_stride_b;
+  g.z_st = d->z_stride_t;
+  g.ab_sb = d->ab_stride_b;
+  g.ab_st = d->ab_stride_t;
+  g.conv_in_sb = d->conv_in_stride_b;
+  g.s_in_sb = d->s_in_stride_b;
+  g.y_sb = d->y_stride_b;
+  g.y_st = d->y_stride_t;
+  g.batch = d->batch;
+  g.t = d->t;
+  g.nk = d->n_k_heads;
+  g.nv = d->n_v_heads;
+  g.kernel = d->conv_kernel;
+  g.conv_dim = 2 * d->n_k_heads * kD + d->n_v_heads * kD;
+  g.n_chunks = (d->t + kC - 1) / kC;
+  g.eps = d->eps;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t conv_items = (int64_t)g.batch * g.t * (g.conv_dim / 8);
+  const int64_t state_items = (int64_t)g.batch * g.conv_dim;
+  const int64_t recs = (int64_t)g.batch * g.nv * g.n_chunks;
+  const int64_t slices = (int64_t)g.batch * g.nv * (kD / kW);
+  const int64_t norm_items = (int64_t)g.batch * g.t * g.nv;
+  if (recs > INT32_MAX || (conv_items + 255) / 256 > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "GDN grid too large");
+  if (d->dtype == CEV_BF16) {
+    hipLaunchKernelGGL(gdn_conv_kernel<__bf16>, dim3((unsigned)((conv_items + 255) / 256)), dim3(256), 0, s, g);
+    hipLaunchKernelGGL(gdn_conv_state_kernel<__bf16>, dim3((unsigned)((state_items + 255) / 256)), dim3(256), 0, s, g);
+    hipLaunchKernelGGL(gdn_prep_kernel<__bf16>, dim3((unsigned)recs), dim3(256), 0, s, g);
+  } else {
+    hipLaunchKernelGGL(gdn_conv_kernel<float>, dim3((unsigned)((conv_items + 255) / 256)), dim3(256), 0, s, g);
+    hipLaunchKernelGGL(gdn_conv_state_kernel<float>, dim3((unsigned)((state_items + 255) / 256)), dim3(256), 0, s, g);
+    hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3((unsigned)recs), dim3(256), 0, s, g);
+  }
+  hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)slices), dim3(256), 0, s, g);
+  if (d->dtype == CEV_BF16)
+    hipLaunchKernelGGL(gdn_norm_kernel<__bf16>, dim3((unsigned)((norm_items + 3) / 4)), dim3(256), 0, s, g);
+  else
+    hipLaunchKernelGGL(gdn_norm_kernel<float>, dim3((unsigned)((norm_items + 3) / 4)), dim3(256), 0, s, g);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "GDN launch: %s", hipGetErrorString(e));
+  return CEV_OK;
+}

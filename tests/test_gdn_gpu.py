@@ -1,0 +1,125 @@
+"""GPU parity of the Gated DeltaNet layer core (cev_gdn_forward through the C
+ABI) against the oracle's restatement of GatedDeltaNet::forward
+(qwen35.rs:414-453, chunk rule qwen35.rs:301-368).
+
+Bars: the chunk rule is f32 in the reference and is checked to 1e-4 max |d|
+(the reference's own chunked-vs-recurrence test allows 2e-4,
+qwen35.rs:776-822; the GPU sums in another order).  In bf16 the layer output
+is cast to bf16 once at the end and is checked to the 2e-2 bf16 bar; the new
+conv state is a copy and must match bit for bit.  At the config-5 size the
+oracle runs on a prefix of the sequence, and the split-sequence property
+(T1 then T2 with the carried states == T1 + T2 at once) covers the rest.
+"""
+import numpy as np
+import pytest
+
+import cev_hip
+from cev_hip import configs
+from helpers import to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _run_gpu(w, inp, device, conv_in=None, s_in=None, t=None, t0=0):
+    """The layer on tokens [t0, t0 + t) of the workload's inputs."""
+    import torch
+    t = w.t if t is None else t
+    sl = slice(t0, t0 + t)
+    dev = lambda x: to_dev(np.ascontiguousarray(x), w.bf16, device)
+    f32 = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(device)
+    layer = cev_hip.GatedDeltaNet(w.batch, t, w.nk, w.nv, w.dk, w.dv, w.kernel, w.eps,
+                                  dtype=torch.bfloat16 if w.bf16 else torch.float32, device=device)
+    y, conv_out, s_out = layer(dev(inp["mixed"][:, sl]), dev(inp["z"][:, sl]), dev(inp["b"][:, sl]), dev(inp["a"][:, sl]),
+                               dev(inp["conv_w"]), f32(inp["neg_a"]), f32(inp["dt_bias"]), f32(inp["norm_w"]),
+                               conv_in=conv_in, s_in=s_in)
+    torch.cuda.synchronize()
+    return y, conv_out, s_out
+
+
+def _run_oracle(orc, w, inp, t=None, conv_in=None, s_in=None):
+    t = w.t if t is None else t
+    return orc.gdn_layer(inp["mixed"][:, :t], inp["z"][:, :t], inp["b"][:, :t], inp["a"][:, :t], inp["conv_w"], inp["neg_a"],
+                         inp["dt_bias"], inp["norm_w"], w.nk, w.nv, w.dk, w.dv, w.eps, w.bf16, conv_in=conv_in, s_in=s_in)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("t", [1, 64, 150])
+def test_gdn_small_vs_oracle(gpu, orc, bf16, t):
+    w = configs.GdnWorkload("gdn-small", 11, bf16, 2, t, nk=2, nv=4)
+    _say(f"test gdn small: bf16={bf16} B={w.batch} T={t} nk={w.nk} nv={w.nv}")
+    inp = w.inputs()
+    y, co, so = _run_gpu(w, inp, gpu)
+    ry, rco, rso = _run_oracle(orc, w, inp)
+    ey = float(np.abs(to_np(y) - ry).max())
+    es = float(np.abs(to_np(so) - rso).max())
+    _say(f"  max|d| y {ey:.3g}  state {es:.3g}")
+    assert np.array_equal(to_np(co), rco)
+    assert es <= F32_TOL
+    assert ey <= (BF16_TOL if bf16 else F32_TOL)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gdn_carried_state_vs_oracle(gpu, orc, bf16):
+    """conv_in / s_in given (a prefix already consumed), one state broadcast
+    to both rows through batch stride 0 (LayerState::broadcast,
+    decoder.rs:74-88, without the copy)."""
+    import torch
+    w = configs.GdnWorkload("gdn-state", 12, bf16, 2, 90, nk=2, nv=4)
+    inp = w.inputs()
+    rng = np.random.default_rng(3)
+    conv_in = rng.standard_normal((1, w.conv_dim, w.kernel - 1)).astype(np.float32)
+    s_in = (0.3 * rng.standard_normal((1, w.nv, w.dk, w.dv))).astype(np.float32)
+    if bf16:
+        conv_in = cev_hip.synth.round_bf16(conv_in)
+    ci = to_dev(conv_in, bf16, gpu).expand(w.batch, -1, -1)
+    si = torch.from_numpy(s_in).to(gpu).expand(w.batch, -1, -1, -1)
+    y, co, so = _run_gpu(w, inp, gpu, conv_in=ci, s_in=si)
+    ry, rco, rso = _run_oracle(orc, w, inp, conv_in=np.repeat(conv_in, 2, 0), s_in=np.repeat(s_in, 2, 0))
+    ey = float(np.abs(to_np(y) - ry).max())
+    es = float(np.abs(to_np(so) - rso).max())
+    _say(f"gdn carried state bf16={bf16}: max|d| y {ey:.3g} state {es:.3g}")
+    assert np.array_equal(to_np(co), rco)
+    assert es <= F32_TOL
+    assert ey <= (BF16_TOL if bf16 else F32_TOL)
+
+
+def test_gdn_c5_heads_vs_oracle(gpu, orc):
+    """Config 5's head layout (Hk 16 -> Hv 32) on the first 256 tokens."""
+    w = configs.c5_gdn(t=256)
+    _say(f"test gdn c5 heads: T={w.t} nk={w.nk} nv={w.nv}")
+    inp = w.inputs()
+    y, co, so = _run_gpu(w, inp, gpu)
+    ry, rco, rso = _run_oracle(orc, w, inp)
+    ey = float(np.abs(to_np(y) - ry).max())
+    es = float(np.abs(to_np(so) - rso).max())
+    _say(f"  max|d| y {ey:.3g}  state {es:.3g}")
+    assert np.array_equal(to_np(co), rco)
+    assert es <= F32_TOL
+    assert ey <= BF16_TOL
+
+
+def test_gdn_c5_split_sequence(gpu):
+    """4096 tokens at once == 2048 + 2048 with the carried conv and recurrent
+    state (size-independent continuation property at the full config-5 size)."""
+    w = configs.c5_gdn()
+    inp = w.inputs()
+    _say(f"test gdn c5 split: T={w.t}")
+    y, co, so = _run_gpu(w, inp, gpu)
+    h = w.t // 2
+    y1, co1, so1 = _run_gpu(w, inp, gpu, t=h)
+    y2, co2, so2 = _run_gpu(w, inp, gpu, t=h, t0=h, conv_in=co1, s_in=so1)
+    full, parts = to_np(y), np.concatenate([to_np(y1), to_np(y2)], 1)
+    es = float(np.abs(to_np(so) - to_np(so2)).max())
+    ey = float(np.abs(full - parts).max())
+    _say(f"  max|d| y {ey:.3g}  state {es:.3g}")
+    assert np.array_equal(to_np(co), to_np(co2))
+    assert np.isfinite(full).all() and np.isfinite(to_np(so)).all()
+    assert es <= F32_TOL
+    assert ey <= BF16_TOL
