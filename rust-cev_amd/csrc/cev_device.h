@@ -8,13 +8,10 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Round-to-nearest-even f32 -> bf16 -> f32 (the value the model dtype holds).
-__device__ __forceinline__ float bf16_round(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float((u | 0x00400000u) & 0xffff0000u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return __uint_as_float(u & 0xffff0000u);
-}
+// Round-to-nearest-even f32 -> bf16 -> f32 (the value the model dtype holds):
+// v_cvt_pk_bf16_f32 (RNE, denormals kept under the kernels' f32 denorm
+// mode) and a shift back.
+__device__ __forceinline__ float bf16_round(float x) { return (float)(__bf16)x; }
 
 __device__ __forceinline__ uint16_t bf16_bits(float x) {
   return (uint16_t)(__float_as_uint(bf16_round(x)) >> 16);

@@ -30,13 +30,21 @@ constexpr int kD = 128;    // head_k_dim = head_v_dim supported here
 constexpr int kW = 16;     // state columns per scan workgroup
 constexpr int kSX = 132;   // LDS row stride (floats) of 128-wide f32 tiles
 constexpr int kSC = 68;    // LDS row stride of 64-wide f32 tiles
-// Per (row, head, chunk) record in the workspace, in floats.
-constexpr int kRecQd = 0;                    // q * e^cum          (64 x 128)
-constexpr int kRecKd = kRecQd + kC * kD;     // k * e^(last - cum) (64 x 128)
-constexpr int kRecKcd = kRecKd + kC * kD;    // k_cumdecay         (64 x 128)
-constexpr int kRecNv = kRecKcd + kC * kD;    // new_values         (64 x 128)
-constexpr int kRecIntra = kRecNv + kC * kD;  // intra              (64 x 64)
-constexpr int kRecDecay = kRecIntra + kC * kC;
+// Per (row, head, chunk) record in the workspace, in floats, stored in the
+// order the scan's MFMAs consume it: lane l of a wave reads 4 consecutive
+// floats (4 k-steps, or the 4 accumulator rows) with one 16-byte load.
+//   Qd  q e^cum           A operand, row tile w:   [w 4][j 8][lane][4] = Qd[16w + l%16][4(4j+e) + l/16]
+//   Kc  k_cumdecay        same layout as Qd
+//   Kd  k e^(last - cum)  A = Kd^T, dk tile ti:    [ti 8][j 4][lane][4] = Kd[4(4j+e) + l/16][16ti + l%16]
+//   In  intra             A operand, row tile w:   [w 4][j 4][lane][4] = In[16w + l%16][4(4j+e) + l/16]
+//   Nv  new_values        accumulator, slice sl:   [sl 8][w 4][lane][4] = Nv[16w + 4(l/16) + e][16sl + l%16]
+//   decay                 e^last
+constexpr int kRecQd = 0;
+constexpr int kRecKc = kRecQd + kC * kD;
+constexpr int kRecKd = kRecKc + kC * kD;
+constexpr int kRecNv = kRecKd + kC * kD;
+constexpr int kRecIn = kRecNv + kC * kD;
+constexpr int kRecDecay = kRecIn + kC * kC;
 constexpr int kRecFloats = kRecDecay + 16;
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
@@ -85,52 +93,113 @@ struct GdnArgs {
 };
 
 // ---------------------------------------------------------------------------
-// conv + SiLU.  Thread = (row, token, 8 channels).  Each product and partial
-// sum is one model-dtype op (decoder.rs:143-150); SiLU is candle's
-// v / (1 + exp(-v)) with each op in the model dtype.
+// conv + SiLU.  Thread = (row, 8 channels, run of kConvRun tokens): the 8 x K
+// weights stay in registers and the last K-1 input rows slide through a
+// register window, so every input row is read once as one 16-byte vector.
+// Each product and partial sum is one model-dtype op (decoder.rs:143-150);
+// SiLU is candle's v / (1 + exp(-v)) with each op in the model dtype.
+constexpr int kConvRun = 16;
+constexpr int kConvMaxK = 8;
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* v);
+template <>
+__device__ __forceinline__ void load8<__bf16>(const __bf16* p, float* v) {
+  const bf16x8 x = *(const bf16x8*)p;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (float)x[e];
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* v) {
+  const f32x4 x = *(const f32x4*)p, y = *(const f32x4*)(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = x[e];
+    v[e + 4] = y[e];
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float* v);
+template <>
+__device__ __forceinline__ void store8<__bf16>(__bf16* p, const float* v) {
+  bf16x8 x;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = (__bf16)v[e];
+  *(bf16x8*)p = x;
+}
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const float* v) {
+  *(f32x4*)p = f32x4{v[0], v[1], v[2], v[3]};
+  *(f32x4*)(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
+
+template <typename T, int K>
+__device__ __forceinline__ void conv_run(const GdnArgs& g, int r, int t0, int c0) {
+  const T* x = (const T*)g.mixed + r * g.mixed_sb;
+  const T* tail = g.conv_in ? (const T*)g.conv_in + r * g.conv_in_sb : nullptr;
+  float w[8][K];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int u = 0; u < K; ++u) w[e][u] = to_f(((const T*)g.conv_w)[(int64_t)(c0 + e) * K + u]);
+  // window[j] = input row t - (K-1) + j for the token t being produced
+  float win[K][8];
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) {
+    const int p = t0 - (K - 1) + j;
+    if (p >= 0) {
+      load8<T>(x + (int64_t)p * g.mixed_st + c0, win[j]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[j][e] = tail ? to_f(tail[(int64_t)(c0 + e) * (K - 1) + (K - 1 + p)]) : 0.0f;
+    }
+  }
+  T* out = (T*)g.conved + ((int64_t)r * g.t + t0) * g.conv_dim + c0;
+  const int n = min(kConvRun, g.t - t0);
+  for (int i = 0; i < n; ++i) {
+    load8<T>(x + (int64_t)(t0 + i) * g.mixed_st + c0, win[K - 1]);
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int u = 0; u < K; ++u) {
+        const float term = rnd<T>(win[u][e] * w[e][u]);
+        acc = u == 0 ? term : rnd<T>(acc + term);
+      }
+      if (sizeof(T) == 2) {
+        const float ex = bf16_round(expf(-acc));
+        const float den = bf16_round(1.0f + ex);
+        y[e] = bf16_round(acc / den);
+      } else {
+        y[e] = acc / (1.0f + expf(-acc));
+      }
+    }
+    store8<T>(out + (int64_t)i * g.conv_dim, y);
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs g) {
   const int64_t cg = g.conv_dim / 8;
+  const int64_t runs = (g.t + kConvRun - 1) / kConvRun;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)g.batch * g.t * cg) return;
+  if (idx >= (int64_t)g.batch * runs * cg) return;
   const int c0 = (int)(idx % cg) * 8;
-  const int64_t rt = idx / cg;
-  const int t = (int)(rt % g.t), r = (int)(rt / g.t);
-  const T* x = (const T*)g.mixed + r * g.mixed_sb;
-  const T* tail = g.conv_in ? (const T*)g.conv_in + r * g.conv_in_sb : nullptr;
-  const T* w = (const T*)g.conv_w;
-  const int K = g.kernel;
-  float acc[8];
-  for (int u = 0; u < K; ++u) {
-    const int p = t + u - (K - 1);  // source token; < 0 reads the conv state
-    float xv[8];
-    if (p >= 0) {
-      const T* xp = x + p * g.mixed_st + c0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xv[e] = to_f(xp[e]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xv[e] = tail ? to_f(tail[(int64_t)(c0 + e) * (K - 1) + (K - 1 + p)]) : 0.0f;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float term = rnd<T>(xv[e] * to_f(w[(int64_t)(c0 + e) * K + u]));
-      acc[e] = u == 0 ? term : rnd<T>(acc[e] + term);
-    }
-  }
-  T* out = (T*)g.conved + ((int64_t)r * g.t + t) * g.conv_dim + c0;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float v = acc[e];
-    float s;
-    if (sizeof(T) == 2) {
-      const float ex = bf16_round(expf(-v));
-      const float den = bf16_round(1.0f + ex);
-      s = bf16_round(v / den);
-    } else {
-      s = v / (1.0f + expf(-v));
-    }
-    out[e] = from_f<T>(s);
+  const int64_t rr = idx / cg;
+  const int t0 = (int)(rr % runs) * kConvRun, r = (int)(rr / runs);
+  switch (g.kernel) {
+    case 2: conv_run<T, 2>(g, r, t0, c0); break;
+    case 3: conv_run<T, 3>(g, r, t0, c0); break;
+    case 4: conv_run<T, 4>(g, r, t0, c0); break;
+    case 5: conv_run<T, 5>(g, r, t0, c0); break;
+    case 6: conv_run<T, 6>(g, r, t0, c0); break;
+    case 7: conv_run<T, 7>(g, r, t0, c0); break;
+    default: conv_run<T, 8>(g, r, t0, c0); break;
   }
 }
 
@@ -156,16 +225,19 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(GdnArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// prep: one workgroup (4 waves) per (row, value head, chunk).
+// prep: one workgroup (8 waves) per (row, value head, chunk).
+constexpr int kPrepThreads = 512;
+constexpr int kPrepWaves = kPrepThreads / 64;
+
 template <typename T>
-__global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
+__global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   __shared__ float Qs[kC * kSX];
   __shared__ float Ks[kC * kSX];
   __shared__ float Vs[kC * kSX];
   __shared__ float Us[kC * kSC];   // strict lower ut
   __shared__ float Iv[kC * kSC];   // (I + Us)^-1
   __shared__ float Tm[kC * kSC];   // products of the block inversion
-  __shared__ float gs[kC], betas[kC], cums[kC];
+  __shared__ float gs[kC], betas[kC], cums[kC], ecum[kC], ekd[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x % g.n_chunks;
@@ -177,18 +249,15 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
 
   // ---- load q, k, v of the chunk (rows past t are the zero padding)
   const T* cv = (const T*)g.conved + (int64_t)r * g.t * g.conv_dim;
-  for (int p = tid; p < kC * (kD / 8); p += 256) {
+  for (int p = tid; p < kC * (kD / 8); p += kPrepThreads) {
     const int i = p / (kD / 8), col = (p % (kD / 8)) * 8;
     const int t = t0 + i;
     float qv[8], kv[8], vv[8];
     if (t < g.t) {
       const T* row = cv + (int64_t)t * g.conv_dim;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        qv[e] = to_f(row[kh * kD + col + e]);
-        kv[e] = to_f(row[key_dim + kh * kD + col + e]);
-        vv[e] = to_f(row[2 * key_dim + h * kD + col + e]);
-      }
+      load8<T>(row + kh * kD + col, qv);
+      load8<T>(row + key_dim + kh * kD + col, kv);
+      load8<T>(row + 2 * key_dim + h * kD + col, vv);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) qv[e] = kv[e] = vv[e] = 0.0f;
@@ -216,9 +285,9 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
   }
   __syncthreads();
 
-  // ---- l2norm of q (then * dk^-0.5) and k rows: wave w takes rows w, w+4, ...
+  // ---- l2norm of q (then * dk^-0.5) and k rows: wave w takes rows w, w+8, ...
   const float qscale = 0.08838834764831845f;  // 128^-0.5
-  for (int i = wave; i < 2 * kC; i += 4) {
+  for (int i = wave; i < 2 * kC; i += kPrepWaves) {
     float* row = i < kC ? Qs + i * kSX : Ks + (i - kC) * kSX;
     const float x0 = row[lane], x1 = row[lane + 64];
     float s = x0 * x0 + x1 * x1;
@@ -237,14 +306,21 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
     }
   }
   __syncthreads();
+  if (tid < kC) {
+    ecum[tid] = expf(cums[tid]);
+    ekd[tid] = expf(cums[kC - 1] - cums[tid]);
+  }
 
   float* rec = g.rec + (int64_t)blockIdx.x * kRecFloats;
   const int fm = lane & 15, fq = lane >> 4;  // fragment row / k-slot of this lane
 
-  // ---- G = K K^T and QK = Q K^T on the lower 16x16 tiles; ut, intra.
-  // Tile list (ti, tj), tj <= ti, dealt round-robin to the waves.
-  for (int tile = wave; tile < 16; tile += 4) {
-    const int ti = tile / 4, tj = tile % 4;
+  // ---- G = K K^T and QK = Q K^T on the 16x16 tiles; ut, intra.  The 10
+  // lower tiles come first in the order below so the waves share them
+  // evenly; the 6 upper tiles only write zeros.
+  for (int tile = wave; tile < 16; tile += kPrepWaves) {
+    constexpr int kOrder[16][2] = {{0, 0}, {1, 0}, {1, 1}, {2, 0}, {2, 1}, {2, 2}, {3, 0}, {3, 1},
+                                   {3, 2}, {3, 3}, {0, 1}, {0, 2}, {0, 3}, {1, 2}, {1, 3}, {2, 3}};
+    const int ti = kOrder[tile][0], tj = kOrder[tile][1];
     f32x4v gacc = {0, 0, 0, 0}, qacc = {0, 0, 0, 0};
     if (tj <= ti) {
       for (int k = 0; k < kD; k += 4) {
@@ -258,31 +334,62 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
       const int i = 16 * ti + 4 * fq + e, j = 16 * tj + fm;
       const float pair = j <= i ? expf(cums[i] - cums[j]) : 0.0f;
       Us[i * kSC + j] = j < i ? betas[i] * gacc[e] * pair : 0.0f;
-      rec[kRecIntra + i * kC + j] = qacc[e] * pair;
+      Tm[i * kSC + j] = qacc[e] * pair;  // intra
     }
   }
   __syncthreads();
+  // intra in A-fragment order: [w 4][j 4][lane][4]
+  for (int p = tid; p < kC * kC / 4; p += kPrepThreads) {
+    const int l = p & 63, j = (p >> 6) & 3, w = p >> 8;
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = Tm[(16 * w + (l & 15)) * kSC + 4 * (4 * j + e) + (l >> 4)];
+    *(f32x4*)(rec + kRecIn + 4 * p) = v;
+  }
+  // q e^cum and k e^(last - cum) in their fragment orders; e^last
+  for (int p = tid; p < kC * kD / 4; p += kPrepThreads) {
+    const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;       // Qd: [w 4][j 8][lane]
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * w + (l & 15), k = 4 * (4 * j + e) + (l >> 4);
+      v[e] = Qs[i * kSX + k] * ecum[i];
+    }
+    *(f32x4*)(rec + kRecQd + 4 * p) = v;
+    const int jj = (p >> 6) & 3, ti = p >> 8;                  // Kd: [ti 8][j 4][lane]
+    f32x4 u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * (4 * jj + e) + (l >> 4), col = 16 * ti + (l & 15);
+      u[e] = Ks[i * kSX + col] * ekd[i];
+    }
+    *(f32x4*)(rec + kRecKd + 4 * p) = u;
+  }
+  if (tid == 0) rec[kRecDecay] = expf(cums[kC - 1]);
+  __syncthreads();  // Tm is reused by the inversion
 
   // ---- inv = (I + L)^-1, L = Us strict lower, by the block recursion of
   // inv_unit_lower (qwen35.rs:277-296) over 16, 32, 64:
   //   [A 0; C B]^-1 = [A^-1 0; -(B^-1 C) A^-1  B^-1].
-  // 16x16 diagonal blocks by forward substitution (wave w, block w).
-  {
-    const int b0 = 16 * wave;
-    const int j = lane & 15;
-    if (lane < 16) {
-      for (int i = 0; i < 16; ++i) Iv[(b0 + i) * kSC + b0 + j] = i == j ? 1.0f : 0.0f;
-    }
+  // 16x16 diagonal blocks by forward substitution, all four in wave 0:
+  // lane 16b + j owns column j of block b in registers,
+  //   inv[i][j] = -sum_{k<i} L[i][k] inv[k][j]  (inv[k][j] = 0 for k < j,
+  //   1 for k == j), the L[i][k] reads being wave-wide broadcasts per block.
+  if (wave == 0) {
+    const int b0 = 16 * (lane >> 4), j = lane & 15;
+    float col[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) col[k] = k == j ? 1.0f : 0.0f;
+#pragma unroll
     for (int i = 1; i < 16; ++i) {
-      // row i = -sum_{k<i} L[i][k] inv[k][:]
-      if (lane < 16 && j < i) {
-        float s = 0.0f;
-        for (int k = j; k < i; ++k) s += Us[(b0 + i) * kSC + b0 + k] * Iv[(b0 + k) * kSC + b0 + j];
-        Iv[(b0 + i) * kSC + b0 + j] = -s;
-      }
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      const float* Lrow = Us + (b0 + i) * kSC + b0;
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < i; ++k) acc += Lrow[k] * col[k];
+      col[i] = i > j ? -acc : col[i];
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Iv[(b0 + i) * kSC + b0 + j] = col[i];
   }
   __syncthreads();
   // 32x32 level: blocks [0,32) (wave 0) and [32,64) (wave 1): off-diagonal
@@ -308,8 +415,8 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
   __syncthreads();
   // 64x64 level: off block (rows 32..63, cols 0..31) = -(B^-1 C) A^-1 with
   // 32x32 A^-1 = Iv[0:32,0:32], B^-1 = Iv[32:64,32:64], C = Us[32:64,0:32].
-  // Wave w computes the 16x16 tile (w/2, w%2) of B^-1 C, then of the product.
-  {
+  // Wave w < 4 computes the 16x16 tile (w/2, w%2) of B^-1 C, then of the product.
+  if (wave < 4) {
     const int ti = wave >> 1, tj = wave & 1;
     f32x4v bc = {0, 0, 0, 0};
     for (int k = 0; k < 32; k += 4)
@@ -318,7 +425,7 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
     for (int e = 0; e < 4; ++e) Tm[(16 * ti + 4 * fq + e) * kSC + 16 * tj + fm] = bc[e];
   }
   __syncthreads();
-  {
+  if (wave < 4) {
     const int ti = wave >> 1, tj = wave & 1;
     f32x4v x = {0, 0, 0, 0};
     for (int k = 0; k < 32; k += 4) x = mma16(Tm[(16 * ti + fm) * kSC + k + fq], Iv[(k + fq) * kSC + 16 * tj + fm], x);
@@ -331,8 +438,10 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
 
   // ---- new_values = inv (v beta), k_cumdecay = inv (k beta e^cum):
   // 4 x 8 output tiles each; the K range of row tile ti stops at its
-  // diagonal block (inv is lower triangular).
-  for (int tile = wave; tile < 32; tile += 4) {
+  // diagonal block (inv is lower triangular).  new_values goes out in the
+  // scan's accumulator order; k_cumdecay is staged in Qs (free now) and
+  // written in A-fragment order.
+  for (int tile = wave; tile < 32; tile += kPrepWaves) {
     const int ti = tile / 8, tn = tile % 8;
     f32x4v nv = {0, 0, 0, 0}, kc = {0, 0, 0, 0};
     for (int k = 0; k < 16 * (ti + 1); k += 4) {
@@ -340,23 +449,20 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
       const int kk = k + fq;
       const float bsc = betas[kk];
       nv = mma16(av, Vs[kk * kSX + 16 * tn + fm] * bsc, nv);
-      kc = mma16(av, Ks[kk * kSX + 16 * tn + fm] * bsc * expf(cums[kk]), kc);
+      kc = mma16(av, Ks[kk * kSX + 16 * tn + fm] * (bsc * ecum[kk]), kc);
     }
+    *(f32x4*)(rec + kRecNv + ((tn * 4 + ti) * 64 + lane) * 4) = f32x4{nv[0], nv[1], nv[2], nv[3]};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * ti + 4 * fq + e, col = 16 * tn + fm;
-      rec[kRecNv + i * kD + col] = nv[e];
-      rec[kRecKcd + i * kD + col] = kc[e];
-    }
+    for (int e = 0; e < 4; ++e) Qs[(16 * ti + 4 * fq + e) * kSX + 16 * tn + fm] = kc[e];
   }
-  // ---- q e^cum, k e^(last - cum), e^last
-  const float last = cums[kC - 1];
-  for (int p = tid; p < kC * kD; p += 256) {
-    const int i = p / kD, col = p % kD;
-    rec[kRecQd + p] = Qs[i * kSX + col] * expf(cums[i]);
-    rec[kRecKd + p] = Ks[i * kSX + col] * expf(last - cums[i]);
+  __syncthreads();
+  for (int p = tid; p < kC * kD / 4; p += kPrepThreads) {
+    const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = Qs[(16 * w + (l & 15)) * kSX + 4 * (4 * j + e) + (l >> 4)];
+    *(f32x4*)(rec + kRecKc + 4 * p) = v;
   }
-  if (tid == 0) rec[kRecDecay] = expf(last);
 }
 
 // ---------------------------------------------------------------------------
@@ -364,87 +470,114 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnArgs g) {
 // state).  Per chunk (qwen35.rs:353-364):
 //   v_new = new_values - k_cumdecay . S;   out = (q e^cum) . S + intra . v_new;
 //   S = S e^last + (k e^(last-cum))^T . v_new.
-__global__ __launch_bounds__(256) void gdn_scan_kernel(GdnArgs g) {
-  __shared__ float Kc[kC * kSX];   // k_cumdecay
-  __shared__ float Qd[kC * kSX];   // q e^cum
-  __shared__ float Kd[kC * kSX];   // k e^(last - cum)
-  __shared__ float In[kC * kSC];   // intra
-  __shared__ float Nv[kC * 20];    // new_values, this slice
-  __shared__ float Vn[kC * 20];    // v_new
-  __shared__ float S[kD * 20];     // state slice (dk x 16)
+// The A operands come straight from the fragment-ordered record (L2), the
+// B operands (S, v_new) from LDS.  blockIdx -> (item, slice) keeps the 8
+// slices of one head on one XCD (workgroups go round-robin over the 8
+// XCDs), so each head's records are fetched into one L2 only.
+constexpr int kXcds = 8;
+constexpr int kScanThreads = 512;
+
+// Wave w = (row tile rt = w % 4, role hf = w / 4): role 0 forms v_new rows
+// 16rt.. (k_cumdecay . S), role 1 the output rows 16rt.. ((q e^cum) . S +
+// intra . v_new); wave w then updates state rows 16w.. .  With kPrefetch
+// (more than one chunk) the operands of chunk c+1 are loaded into
+// registers while chunk c computes.
+template <bool kPrefetch>
+__global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
+  __shared__ float S[kD * 20];   // state slice (dk x 16)
+  __shared__ float Vn[kC * 20];  // v_new
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nslice = kD / kW;
-  const int sl = blockIdx.x % nslice;
-  const int hr = blockIdx.x / nslice;
-  const int h = hr % g.nv, r = hr / g.nv;
+  const int rt = wave & 3, hf = wave >> 2;
+  constexpr int nslice = kD / kW;
+  const int b = blockIdx.x;
+  const int item = (b % kXcds) + kXcds * (b / (kXcds * nslice));  // (row, head) index
+  const int sl = (b / kXcds) % nslice;
+  if (item >= g.batch * g.nv) return;
+  const int h = item % g.nv, r = item / g.nv;
   const int col0 = sl * kW;
   const int fm = lane & 15, fq = lane >> 4;
 
-  for (int p = tid; p < kD * kW; p += 256) {
+  for (int p = tid; p < kD * kW; p += kScanThreads) {
     const int i = p / kW, j = p % kW;
     S[i * 20 + j] = g.s_in ? g.s_in[r * g.s_in_sb + ((int64_t)h * kD + i) * kD + col0 + j] : 0.0f;
   }
-  for (int c = 0; c < g.n_chunks; ++c) {
-    const float* rec = g.rec + ((int64_t)hr * g.n_chunks + c) * kRecFloats;
-    for (int p = tid; p < kC * kD / 4; p += 256) {
-      const int i = p / (kD / 4), col = (p % (kD / 4)) * 4;
-      const f32x4 q = *(const f32x4*)(rec + kRecQd + i * kD + col);
-      const f32x4 kd = *(const f32x4*)(rec + kRecKd + i * kD + col);
-      const f32x4 kc = *(const f32x4*)(rec + kRecKcd + i * kD + col);
+  __syncthreads();
+  struct Ops {
+    f32x4 a[8], ia[4], d[4], nvv;
+    float decay;
+  };
+  auto fetch = [&](int c, Ops& o) {
+    const float* rec = g.rec + ((int64_t)item * g.n_chunks + c) * kRecFloats;
+    const f32x4* ap = (const f32x4*)(rec + (hf ? kRecQd : kRecKc)) + rt * 8 * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o.a[j] = ap[j * 64];
+    if (hf) {
+      const f32x4* inp = (const f32x4*)(rec + kRecIn) + rt * 4 * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o.ia[j] = inp[j * 64];
+    } else {
+      o.nvv = *((const f32x4*)(rec + kRecNv) + (sl * 4 + rt) * 64 + lane);
+    }
+    const f32x4* kdp = (const f32x4*)(rec + kRecKd) + wave * 4 * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.d[j] = kdp[j * 64];
+    o.decay = rec[kRecDecay];
+  };
+  auto chunk = [&](int c, Ops& cur, Ops& nxt) {
+    if (kPrefetch && c + 1 < g.n_chunks) fetch(c + 1, nxt);
+    // phase 1: K = dk chain against the state slice
+    f32x4v acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = mma16(cur.a[j][e], S[(4 * (4 * j + e) + fq) * 20 + fm], acc);
+    if (!hf) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Vn[(16 * rt + 4 * fq + e) * 20 + fm] = cur.nvv[e] - acc[e];
+    }
+    __syncthreads();
+    // phase 2: intra . v_new (intra is lower triangular: K stops at the
+    // diagonal block), then this wave's 16 state rows
+    if (hf) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j <= rt) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = mma16(cur.ia[j][e], Vn[(4 * (4 * j + e) + fq) * 20 + fm], acc);
+        }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        Qd[i * kSX + col + e] = q[e];
-        Kd[i * kSX + col + e] = kd[e];
-        Kc[i * kSX + col + e] = kc[e];
+        const int t = c * kC + 16 * rt + 4 * fq + e;
+        if (t < g.t) g.core[(((int64_t)r * g.t + t) * g.nv + h) * kD + col0 + fm] = acc[e];
       }
     }
-    for (int p = tid; p < kC * kC / 4; p += 256) {
-      const int i = p / (kC / 4), col = (p % (kC / 4)) * 4;
-      const f32x4 v = *(const f32x4*)(rec + kRecIntra + i * kC + col);
+    f32x4v su = {0, 0, 0, 0};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) In[i * kSC + col + e] = v[e];
-    }
-    for (int p = tid; p < kC * kW; p += 256) {
-      const int i = p / kW, j = p % kW;
-      Nv[i * 20 + j] = rec[kRecNv + i * kD + col0 + j];
-    }
-    const float decay = rec[kRecDecay];
-    __syncthreads();
-
-    // phase 1: wave w owns rows 16w..16w+15 of v_new and of out
-    f32x4v kS = {0, 0, 0, 0}, qS = {0, 0, 0, 0};
-    for (int k = 0; k < kD; k += 4) {
-      const float b = S[(k + fq) * 20 + fm];
-      kS = mma16(Kc[(16 * wave + fm) * kSX + k + fq], b, kS);
-      qS = mma16(Qd[(16 * wave + fm) * kSX + k + fq], b, qS);
-    }
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) su = mma16(cur.d[j][e], Vn[(4 * (4 * j + e) + fq) * 20 + fm], su);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int i = 16 * wave + 4 * fq + e;
-      Vn[i * 20 + fm] = Nv[i * 20 + fm] - kS[e];
+      const int r0 = 16 * wave + 4 * fq + e;
+      S[r0 * 20 + fm] = S[r0 * 20 + fm] * cur.decay + su[e];
     }
     __syncthreads();
-    // phase 2: out rows of wave w; S rows 32w..32w+31
-    for (int k = 0; k < 16 * (wave + 1); k += 4) qS = mma16(In[(16 * wave + fm) * kSC + k + fq], Vn[(k + fq) * 20 + fm], qS);
-    f32x4v s0 = {0, 0, 0, 0}, s1 = {0, 0, 0, 0};
-    for (int k = 0; k < kC; k += 4) {
-      const float b = Vn[(k + fq) * 20 + fm];
-      s0 = mma16(Kd[(k + fq) * kSX + 32 * wave + fm], b, s0);
-      s1 = mma16(Kd[(k + fq) * kSX + 32 * wave + 16 + fm], b, s1);
+  };
+  Ops ops_a, ops_b;  // the two register sets alternate (no copy between chunks)
+  fetch(0, ops_a);
+  if constexpr (kPrefetch) {
+    for (int c = 0; c < g.n_chunks; c += 2) {
+      chunk(c, ops_a, ops_b);
+      if (c + 1 < g.n_chunks) chunk(c + 1, ops_b, ops_a);
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * wave + 4 * fq + e;
-      const int t = c * kC + i;
-      if (t < g.t) g.core[(((int64_t)r * g.t + t) * g.nv + h) * kD + col0 + fm] = qS[e];
-      const int r0 = 32 * wave + 4 * fq + e;
-      S[r0 * 20 + fm] = S[r0 * 20 + fm] * decay + s0[e];
-      S[(r0 + 16) * 20 + fm] = S[(r0 + 16) * 20 + fm] * decay + s1[e];
+  } else {
+    for (int c = 0; c < g.n_chunks; ++c) {
+      if (c > 0) fetch(c, ops_a);
+      chunk(c, ops_a, ops_a);
     }
-    __syncthreads();
   }
-  for (int p = tid; p < kD * kW; p += 256) {
+  for (int p = tid; p < kD * kW; p += kScanThreads) {
     const int i = p / kW, j = p % kW;
     g.s_out[((int64_t)r * g.nv + h) * kD * kD + (int64_t)i * kD + col0 + j] = S[i * 20 + j];
   }
@@ -461,20 +594,21 @@ __global__ __launch_bounds__(256) void gdn_norm_kernel(GdnArgs g) {
   const int h = (int)(item % g.nv);
   const int64_t rt = item / g.nv;
   const int t = (int)(rt % g.t), r = (int)(rt / g.t);
-  const float* cr = g.core + item * kD;
-  const float c0 = cr[lane], c1 = cr[lane + 64];
-  float s = c0 * c0 + c1 * c1;
+  // lane holds head-dim elements 2 lane, 2 lane + 1
+  const float2 cv = *(const float2*)(g.core + item * kD + 2 * lane);
+  float s = cv.x * cv.x + cv.y * cv.y;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
   const float den = sqrtf(s / (float)kD + g.eps);
-  const T* zr = (const T*)g.z + r * g.z_sb + (int64_t)t * g.z_st + h * kD;
-  T* yr = (T*)g.y + r * g.y_sb + (int64_t)t * g.y_st + h * kD;
+  const T* zr = (const T*)g.z + r * g.z_sb + (int64_t)t * g.z_st + h * kD + 2 * lane;
+  T* yr = (T*)g.y + r * g.y_sb + (int64_t)t * g.y_st + h * kD + 2 * lane;
+  const float2 wv = *(const float2*)(g.norm_w + 2 * lane);
+  const float c2[2] = {cv.x, cv.y}, w2[2] = {wv.x, wv.y};
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const int i = lane + 64 * e;
-    const float zz = to_f(zr[i]);
+    const float zz = to_f(zr[e]);
     const float gate = zz / (1.0f + expf(-zz));
-    yr[i] = from_f<T>((e ? c1 : c0) / den * g.norm_w[i] * gate);
+    yr[e] = from_f<T>(c2[e] / den * w2[e] * gate);
   }
 }
 
@@ -570,6 +704,7 @@ extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, con
   CEV_CHECK_ARG(((uintptr_t)mixed & al) == 0 && (d->mixed_stride_t % 8) == 0 && (d->mixed_stride_b % 8) == 0,
                 "cev_gdn_forward: the conv input rows must be 8-element aligned");
   CEV_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "cev_gdn_forward: workspace must be 256-byte aligned");
+  CEV_CHECK_ARG(((uintptr_t)norm_w & 7) == 0, "cev_gdn_forward: norm_w must be 8-byte aligned");
   GdnArgs g;
   g.mixed = mixed;
   g.z = z;
@@ -606,22 +741,25 @@ extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, con
   g.n_chunks = (d->t + kC - 1) / kC;
   g.eps = d->eps;
   hipStream_t s = (hipStream_t)stream;
-  const int64_t conv_items = (int64_t)g.batch * g.t * (g.conv_dim / 8);
+  const int64_t conv_items = (int64_t)g.batch * ((g.t + kConvRun - 1) / kConvRun) * (g.conv_dim / 8);
   const int64_t state_items = (int64_t)g.batch * g.conv_dim;
   const int64_t recs = (int64_t)g.batch * g.nv * g.n_chunks;
-  const int64_t slices = (int64_t)g.batch * g.nv * (kD / kW);
+  const int64_t slices = ((int64_t)g.batch * g.nv + kXcds - 1) / kXcds * kXcds * (kD / kW);
   const int64_t norm_items = (int64_t)g.batch * g.t * g.nv;
   if (recs > INT32_MAX || (conv_items + 255) / 256 > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "GDN grid too large");
   if (d->dtype == CEV_BF16) {
     hipLaunchKernelGGL(gdn_conv_kernel<__bf16>, dim3((unsigned)((conv_items + 255) / 256)), dim3(256), 0, s, g);
     hipLaunchKernelGGL(gdn_conv_state_kernel<__bf16>, dim3((unsigned)((state_items + 255) / 256)), dim3(256), 0, s, g);
-    hipLaunchKernelGGL(gdn_prep_kernel<__bf16>, dim3((unsigned)recs), dim3(256), 0, s, g);
+    hipLaunchKernelGGL(gdn_prep_kernel<__bf16>, dim3((unsigned)recs), dim3(kPrepThreads), 0, s, g);
   } else {
     hipLaunchKernelGGL(gdn_conv_kernel<float>, dim3((unsigned)((conv_items + 255) / 256)), dim3(256), 0, s, g);
     hipLaunchKernelGGL(gdn_conv_state_kernel<float>, dim3((unsigned)((state_items + 255) / 256)), dim3(256), 0, s, g);
-    hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3((unsigned)recs), dim3(256), 0, s, g);
+    hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3((unsigned)recs), dim3(kPrepThreads), 0, s, g);
   }
-  hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)slices), dim3(256), 0, s, g);
+  if (g.n_chunks > 1)
+    hipLaunchKernelGGL(gdn_scan_kernel<true>, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
+  else
+    hipLaunchKernelGGL(gdn_scan_kernel<false>, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
   if (d->dtype == CEV_BF16)
     hipLaunchKernelGGL(gdn_norm_kernel<__bf16>, dim3((unsigned)((norm_items + 3) / 4)), dim3(256), 0, s, g);
   else
