@@ -51,11 +51,25 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def _sample_rows(run, total: int, step: int, target_s: float):
+    """Times run(rows) once on `step` rows (warm-up), sizes a sample of about
+    target_s seconds in multiples of `step`, and returns (rows, median s of 5)."""
+    _, t1 = run(step)
+    n = int(max(1, min(total // step, round(target_s / max(t1, 1e-3)))))
+    times, rows = [], 0
+    for _ in range(5):
+        rows, dt = run(n * step)
+        times.append(dt)
+    return rows, statistics.median(times)
+
+
 def cpu_baseline(w, np_inputs, target_s: float = 3.0):
-    """The oracle's restatement of the reference's CPU path (candle op order:
-    q/k RMSNorm + RoPE, repeat_kv, dense q.k^T over every key, additive
-    engine mask, softmax, bf16 rounding points, p.v) on the rows of the first
-    n blocks.  The dense mask is built once outside the timed region."""
+    """The oracle's restatement of the reference's CPU path on the first rows
+    of the suffix, in candle's op order: q/k RMSNorm + RoPE, repeat_kv, dense
+    q.k^T over every key, the additive mask the reference builds for this
+    layer (the engine's packed mask for causal blocks, the bidirectional row
+    mask otherwise), softmax, bf16 rounding points, p.v and, for a gated
+    layer, the sigmoid gate.  Masks are built once outside the timed region."""
     import numpy as np
 
     import oracle
@@ -69,33 +83,160 @@ def cpu_baseline(w, np_inputs, target_s: float = 3.0):
     kall = np.concatenate([pk, kr.transpose(1, 0, 2)], axis=1) if w.prefix else np.ascontiguousarray(kr.transpose(1, 0, 2))
     vall = np.concatenate([pv, v.transpose(1, 0, 2)], axis=1) if w.prefix else np.ascontiguousarray(v.transpose(1, 0, 2))
     t_mask = time.perf_counter()
-    plans, items = w.plans_items()
-    mask = oracle.engine_pass(plans, items)["mask"]
+    if w.causal:
+        plans, items = w.plans_items()
+        mask, mask_kind = oracle.engine_pass(plans, items)["mask"], "engine packed mask"
+    else:
+        assert len(w.blocks) == 1 and not w.prefix
+        mask, mask_kind = oracle.bidirectional_mask(w.t, [w.lengths[0]])[0], "bidirectional row mask"
     mask_s = time.perf_counter() - t_mask
 
-    def run(nb):
-        rows = int(sum(w.blocks[:nb]))
+    def run(rows):
         t0 = time.perf_counter()
-        qs = oracle.rope(oracle.rms_norm(q[:rows, :, :d], wq, w.eps, bf, plus_one=w.plus_one), pos[:rows], cos, sin, w.rotary_dim, bf)
-        oracle.attend(np.ascontiguousarray(qs.transpose(1, 0, 2)), kall, vall, mask[:rows], bf)
+        qs = oracle.rope(oracle.rms_norm(q[:rows, :, :d], wq, w.eps, bf, plus_one=w.plus_one), pos[:rows], cos, sin,
+                         w.rotary_dim, bf)
+        out = oracle.attend(np.ascontiguousarray(qs.transpose(1, 0, 2)), kall, vall, mask[:rows], bf)
+        if w.gated:
+            o = np.ascontiguousarray(out[0].transpose(1, 0, 2)).reshape(rows, -1)
+            oracle.sigmoid_gate(o, np.ascontiguousarray(q[:rows, :, d:]).reshape(rows, -1), bf)
         return rows, time.perf_counter() - t0
 
-    _, t1 = run(1)  # warm-up, sizes the sample
-    nb = int(max(1, min(len(w.blocks), round(target_s / max(t1, 1e-3)))))
-    times, rows = [], 0
-    for _ in range(5):
-        rows, dt = run(nb)
-        times.append(dt)
-    med = statistics.median(times)
+    step = w.blocks[0] if w.causal else 64
+    rows, med = _sample_rows(run, w.t, step, target_s)
     return {
         "value": rows / med,
         "unit": "query tok/s",
         "cores": oracle.threads(),
         "kind": "port",
-        "sample": (f"rows of the first {nb} of {len(w.blocks)} suffix blocks ({rows} query rows x {w.hq} heads) through the oracle's "
-                   f"candle-op restatement over all {w.prefix + w.t} keys with the dense engine mask; median of 5 runs after a warm-up; "
-                   f"dense mask build {mask_s * 1e3:.0f} ms excluded; CPU: {cpu_model()}"),
+        "sample": (f"the first {rows} of {w.t} suffix query rows x {w.hq} heads through the oracle's candle-op restatement "
+                   f"over all {w.prefix + w.t} keys with the dense {mask_kind}; median of 5 runs after a warm-up; mask build "
+                   f"{mask_s * 1e3:.0f} ms excluded; CPU: {cpu_model()}"),
     }
+
+
+def cpu_baseline_gdn(w, inp, target_s: float = 3.0):
+    """The oracle's restatement of GatedDeltaNet::forward between the input
+    projections and out_proj (conv + SiLU, gates, chunk_gated_delta_rule,
+    gated RMSNorm) on the first tokens of row 0."""
+    import oracle
+    if not os.path.exists(oracle.LIB_PATH):
+        oracle.build()
+
+    def run(n):
+        t0 = time.perf_counter()
+        oracle.gdn_layer(inp["mixed"][:1, :n], inp["z"][:1, :n], inp["b"][:1, :n], inp["a"][:1, :n], inp["conv_w"],
+                         inp["neg_a"], inp["dt_bias"], inp["norm_w"], w.nk, w.nv, w.dk, w.dv, w.eps, w.bf16)
+        return n, time.perf_counter() - t0
+
+    n, med = _sample_rows(run, w.t, 64, target_s)
+    return {
+        "value": n / med,
+        "unit": "tok/s",
+        "cores": oracle.threads(),
+        "kind": "port",
+        "sample": (f"the first {n} of {w.t} tokens of one row ({w.nv} value heads) through the oracle's restatement of the "
+                   f"layer (conv + SiLU, gates, 64-token chunked delta rule, gated RMSNorm); median of 5 runs after a "
+                   f"warm-up; CPU: {cpu_model()}"),
+    }
+
+
+def roofline(flops: float, alg: int, ms: float, dtype: str, kernel: str, traffic):
+    intensity = flops / alg
+    ridge = PEAK_TFLOPS[dtype] * 1e12 / (PEAK_HBM_GBPS * 1e9)
+    if intensity >= ridge:
+        roof = {"bound": "mfma", "achieved": flops / (ms * 1e-3) / 1e12, "peak": PEAK_TFLOPS[dtype], "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": alg / (ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBPS, "unit": "GB/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["traffic"] = traffic
+    roof["kernel"] = kernel
+    roof["kernel_ms"] = ms
+    roof["alg_bytes"] = alg
+    roof["useful_flop"] = flops
+    return roof
+
+
+def calibrate_gemm(n: int, steps: int, warmup: int):
+    """The practical bf16 MFMA ceiling on this card: hipBLASLt's n^3 GEMM
+    (torch.matmul) on random N(0,1) operands and on all-zero operands.  The
+    gap between the two is the power limit that random data hits."""
+    import torch
+    dev = torch.device("cuda:0")
+    out = {"calibrate_gemm": n}
+    for name, make in (("random", torch.randn), ("zeros", torch.zeros)):
+        a = make((n, n), dtype=torch.bfloat16, device=dev)
+        b = make((n, n), dtype=torch.bfloat16, device=dev)
+        for _ in range(warmup):
+            torch.matmul(a, b)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            torch.matmul(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        out[name] = {"ms": ms, "tflops": 2.0 * n ** 3 / (ms * 1e-3) / 1e12}
+    print(json.dumps(out), flush=True)
+
+
+def bench_gdn(args, w, dev):
+    """One step = the GatedDeltaNet layer core (four kernels) over the batch."""
+    import numpy as np
+    import torch
+
+    import cev_hip
+    from cev_hip import device_info
+    inp = w.inputs()
+    mdt = torch.bfloat16 if w.bf16 else torch.float32
+
+    def d(x):
+        return torch.from_numpy(np.ascontiguousarray(x)).to(dev).to(mdt)
+
+    def f(x):
+        return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev)
+
+    layer = cev_hip.GatedDeltaNet(w.batch, w.t, w.nk, w.nv, w.dk, w.dv, w.kernel, w.eps, dtype=mdt, device=dev)
+    xs = [d(inp[k]) for k in ("mixed", "z", "b", "a", "conv_w")] + [f(inp[k]) for k in ("neg_a", "dt_bias", "norm_w")]
+    s_in = None
+    if w.batch > 1:
+        s_in = torch.zeros((1, w.nv, w.dk, w.dv), device=dev).expand(w.batch, -1, -1, -1)
+    y = torch.empty((w.batch, w.t, w.nv * w.dv), dtype=mdt, device=dev)
+    conv_out = torch.empty((w.batch, w.conv_dim, w.kernel - 1), dtype=mdt, device=dev)
+    s_out = torch.empty((w.batch, w.nv, w.dk, w.dv), dtype=torch.float32, device=dev)
+    for _ in range(args.warmup):
+        layer(*xs, s_in=s_in, y=y, conv_out=conv_out, s_out=s_out)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record()
+        layer(*xs, s_in=s_in, y=y, conv_out=conv_out, s_out=s_out)
+        b.record()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    layer_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    esz = 2 if w.bf16 else 4
+    tok = w.batch * w.t
+    alg = (tok * (w.conv_dim + 2 * w.nv * w.dv + 2 * w.nv) * esz + w.batch * w.nv * w.dk * w.dv * 4 * (2 if s_in is not None else 1)
+           + w.batch * w.conv_dim * (w.kernel - 1) * esz)
+    res = {
+        "metric": "Gated DeltaNet layer core tok/s and % f32 MFMA peak on 1 MI355X",
+        "value": tok / (ms_step * 1e-3),
+        "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded projection outputs; beta uniform in (0,1), decay log-uniform in [1e-3, 1])",
+        "config": {"workload": f"{w.name}: Gated DeltaNet layer, batch {w.batch} x {w.t} tokens, Hk={w.nk} Hv={w.nv} "
+                               f"dk={w.dk} dv={w.dv}, conv kernel {w.kernel}, 64-token chunks, "
+                               f"{'bf16' if w.bf16 else 'f32'} inputs, f32 chunk rule"},
+        "roofline": roofline(w.flops(), alg, layer_ms, "f32", "gdn conv + prep + scan + norm (one forward call)", None),
+        "device": device_info().name,
+    }
+    if args.cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_gdn(w, inp)
+    print(json.dumps(res), flush=True)
 
 
 def main():
@@ -103,11 +244,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "c4", "c5a", "hbm"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "c4", "c5a", "hbm", "c5gdn", "c5gdnrows"],
+                    help="c3 (default): the 32k-prefix packed-prefill attention; c5gdn / c5gdnrows: the Gated DeltaNet "
+                         "layer core over one 4096-token row / 32 rows of 64 tokens")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline leg")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the workload, run `steps` device copies of MIB MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes)")
+    ap.add_argument("--calibrate-gemm", type=int, default=0, metavar="N",
+                    help="instead of the workload, time torch.matmul bf16 N^3 on random and on zero operands")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -121,6 +266,15 @@ def main():
     from cev_hip.layer import AttentionLayer
 
     dev = torch.device("cuda:0")
+    if args.calibrate_gemm:
+        calibrate_gemm(args.calibrate_gemm, args.steps, args.warmup)
+        return
+    if args.workload == "c5gdn":
+        bench_gdn(args, configs.c5_gdn(), dev)
+        return
+    if args.workload == "c5gdnrows":
+        bench_gdn(args, configs.GdnWorkload("c5gdn32x64", 5, True, 32, 64), dev)
+        return
     if args.calibrate_copy:
         n = args.calibrate_copy << 20
         src = torch.ones(n, dtype=torch.uint8, device=dev)
@@ -153,19 +307,8 @@ def main():
 
     dtype = "bf16" if w.bf16 else "f32"
     flops = w.useful_flops()
-    alg = w.alg_bytes()
-    intensity = flops / alg
-    ridge = PEAK_TFLOPS[dtype] * 1e12 / (PEAK_HBM_GBPS * 1e9)
-    if intensity >= ridge:
-        roof = {"bound": "mfma", "achieved": flops / (k2_ms * 1e-3) / 1e12, "peak": PEAK_TFLOPS[dtype], "unit": "TFLOP/s"}
-    else:
-        roof = {"bound": "hbm", "achieved": alg / (k2_ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBPS, "unit": "GB/s"}
-    roof["frac"] = roof["achieved"] / roof["peak"]
-    roof["traffic"] = traffic_from_profiles(w.name)
-    roof["kernel"] = "attn_bf16_kernel" if w.bf16 else "attn_f32_kernel"
-    roof["kernel_ms"] = k2_ms
-    roof["alg_bytes"] = alg
-    roof["useful_flop"] = flops
+    kernel = "attn_kernel_pipe<bf16,128>" if (w.bf16 and w.d == 128) else f"attn_kernel_seq<{dtype},{w.d}>"
+    roof = roofline(flops, w.alg_bytes(), k2_ms, dtype, kernel, traffic_from_profiles(w.name))
 
     res = {
         "metric": METRIC,

@@ -186,9 +186,9 @@ int32_t cev_rope_table(double theta, int32_t rotary_dim, int32_t n_pos, int32_t 
 /* Gated DeltaNet layer core (Qwen3.5 linear-attention layers): replaces
  * GatedDeltaNet::forward (crates/cev-model/src/qwen35.rs:414-453) between
  * the input projections and out_proj, i.e. the depthwise conv + SiLU with
- * its state (qwen35.rs:424-428, decoder.rs:137-151), l2norm / sigmoid /
+ * its state (qwen35.rs:428-430, decoder.rs:137-151), l2norm / sigmoid /
  * softplus gates, chunk_gated_delta_rule (qwen35.rs:301-368) and the gated
- * RMSNorm (qwen35.rs:443-449). */
+ * RMSNorm (qwen35.rs:447-451). */
 typedef struct cev_gdn_desc {
   int32_t dtype;       /* model dtype: projections, conv weight, conv state, y */
   int32_t batch;       /* rows B */
@@ -218,7 +218,7 @@ int32_t cev_gdn_workspace_size(const cev_gdn_desc* d, size_t* bytes);
  * conv_in and y are in the model dtype; neg_a = -exp(A_log), dt_bias and
  * norm_w are f32 (as GatedDeltaNet::new holds them, qwen35.rs:393-395);
  * s_in / s_out are (B, nv, dk, dv) f32.  conv_in == NULL / s_in == NULL
- * start from zero state (qwen35.rs:422).  conv_out is (B, conv_dim, K-1)
+ * start from zero state (qwen35.rs:426).  conv_out is (B, conv_dim, K-1)
  * contiguous.  Workspace of cev_gdn_workspace_size bytes, 256-byte
  * aligned. */
 int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, const void* z, const void* b, const void* a, const void* conv_w,

@@ -315,7 +315,7 @@ def gdn_recurrence(qn, kn, v, g, beta, s0=None):
 
 
 def conv_silu(x, tail, w, bf16: bool):
-    """Depthwise conv over [tail || x] + SiLU and the new tail (qwen35.rs:419-431)."""
+    """Depthwise conv over [tail || x] + SiLU and the new tail (qwen35.rs:428-430)."""
     x = _c(x)
     c, t = x.shape
     kw = w.shape[-1]
@@ -328,7 +328,7 @@ def conv_silu(x, tail, w, bf16: bool):
 
 
 def gated_rmsnorm(core, z, w, eps: float, bf16: bool):
-    """qwen35.rs:443-449: core / sqrt(mean core^2 + eps) * w * silu(z), rows of dv."""
+    """qwen35.rs:447-451: core / sqrt(mean core^2 + eps) * w * silu(z), rows of dv."""
     core, z, w = _c(core), _c(z), _c(w)
     dv = core.shape[-1]
     y = np.empty_like(core)

@@ -9,8 +9,8 @@
  *   softplus                   qwen35.rs:243-248
  *   inv_unit_lower             qwen35.rs:256-296 (recursive block inversion)
  *   chunk_gated_delta_rule     qwen35.rs:298-368
- *   depthwise conv + conv tail qwen35.rs:419-431, decoder.rs:137-151
- *   gated RMSNorm . SiLU(z)    qwen35.rs:443-449
+ *   depthwise conv + conv tail qwen35.rs:428-430, decoder.rs:137-151
+ *   gated RMSNorm . SiLU(z)    qwen35.rs:447-451
  *   the token recurrence used by the reference's own check, qwen35.rs:776-822
  *
  * Parity unpinned (no offline reference test covers them): the bf16
@@ -122,125 +122,133 @@ void orc_chunk_gated_delta_rule(const float* q_in, const float* k_in, const floa
   const int n = tp / C;
   const float qscale = (float)pow((double)dk, -0.5);
   int mut_no_decay = orc_get_mutation() == MUT_GDN_NO_DECAY;
-  float* q = (float*)calloc((size_t)tp * dk, sizeof(float));
-  float* k = (float*)calloc((size_t)tp * dk, sizeof(float));
-  float* vb = (float*)calloc((size_t)tp * dv, sizeof(float));
-  float* kb = (float*)calloc((size_t)tp * dk, sizeof(float));
-  float* gp = (float*)calloc((size_t)tp, sizeof(float));
-  float* cum = (float*)malloc(sizeof(float) * (size_t)tp);
-  float* pair = (float*)malloc(sizeof(float) * (size_t)C * C);
-  float* ut = (float*)malloc(sizeof(float) * (size_t)C * C);
-  float* intra = (float*)malloc(sizeof(float) * (size_t)n * C * C);
-  float* inv = (float*)malloc(sizeof(float) * (size_t)C * C);
-  float* nv = (float*)malloc(sizeof(float) * (size_t)tp * dv);
-  float* kcd = (float*)malloc(sizeof(float) * (size_t)tp * dk);
-  float* dkb = (float*)malloc(sizeof(float) * (size_t)C * dk);
-  float* S = (float*)malloc(sizeof(float) * (size_t)dk * dv);
-  float* vnew = (float*)malloc(sizeof(float) * (size_t)C * dv);
-  float* tmp = (float*)malloc(sizeof(float) * (size_t)C * (dv > dk ? dv : dk));
-  for (int hh = 0; hh < h; ++hh) {
-    const float* qh = q_in + (int64_t)hh * t * dk;
-    const float* kh = k_in + (int64_t)hh * t * dk;
-    const float* vh = v + (int64_t)hh * t * dv;
-    const float* gh = g + (int64_t)hh * t;
-    const float* bh = beta + (int64_t)hh * t;
-    memset(q, 0, sizeof(float) * (size_t)tp * dk);
-    memset(k, 0, sizeof(float) * (size_t)tp * dk);
-    memset(vb, 0, sizeof(float) * (size_t)tp * dv);
-    memset(kb, 0, sizeof(float) * (size_t)tp * dk);
-    memset(gp, 0, sizeof(float) * (size_t)tp);
-    orc_l2norm(qh, t, dk, q);
-    for (int64_t i = 0; i < (int64_t)t * dk; ++i) q[i] = q[i] * qscale + 0.0f;
-    orc_l2norm(kh, t, dk, k);
-    for (int i = 0; i < t; ++i) {
-      for (int e = 0; e < dv; ++e) vb[(int64_t)i * dv + e] = vh[(int64_t)i * dv + e] * bh[i];
-      for (int e = 0; e < dk; ++e) kb[(int64_t)i * dk + e] = k[(int64_t)i * dk + e] * bh[i];
-      gp[i] = gh[i];
-    }
-    for (int c = 0; c < n; ++c) {
-      float acc = 0.0f;
-      for (int i = 0; i < C; ++i) {
-        acc += gp[c * C + i];
-        cum[c * C + i] = acc;
+  /* Heads are independent: one thread per head, each with its own scratch. */
+#pragma omp parallel
+  {
+    float* q = (float*)calloc((size_t)tp * dk, sizeof(float));
+    float* k = (float*)calloc((size_t)tp * dk, sizeof(float));
+    float* vb = (float*)calloc((size_t)tp * dv, sizeof(float));
+    float* kb = (float*)calloc((size_t)tp * dk, sizeof(float));
+    float* gp = (float*)calloc((size_t)tp, sizeof(float));
+    float* cum = (float*)malloc(sizeof(float) * (size_t)tp);
+    float* pair = (float*)malloc(sizeof(float) * (size_t)C * C);
+    float* ut = (float*)malloc(sizeof(float) * (size_t)C * C);
+    float* intra = (float*)malloc(sizeof(float) * (size_t)n * C * C);
+    float* inv = (float*)malloc(sizeof(float) * (size_t)C * C);
+    float* nv = (float*)malloc(sizeof(float) * (size_t)tp * dv);
+    float* kcd = (float*)malloc(sizeof(float) * (size_t)tp * dk);
+    float* dkb = (float*)malloc(sizeof(float) * (size_t)C * dk);
+    float* S = (float*)malloc(sizeof(float) * (size_t)dk * dv);
+    float* vnew = (float*)malloc(sizeof(float) * (size_t)C * dv);
+    float* tmp = (float*)malloc(sizeof(float) * (size_t)C * (dv > dk ? dv : dk));
+    float* wdec = (float*)malloc(sizeof(float) * (size_t)C);
+#pragma omp for schedule(dynamic, 1)
+    for (int hh = 0; hh < h; ++hh) {
+      const float* qh = q_in + (int64_t)hh * t * dk;
+      const float* kh = k_in + (int64_t)hh * t * dk;
+      const float* vh = v + (int64_t)hh * t * dv;
+      const float* gh = g + (int64_t)hh * t;
+      const float* bh = beta + (int64_t)hh * t;
+      memset(q, 0, sizeof(float) * (size_t)tp * dk);
+      memset(k, 0, sizeof(float) * (size_t)tp * dk);
+      memset(vb, 0, sizeof(float) * (size_t)tp * dv);
+      memset(kb, 0, sizeof(float) * (size_t)tp * dk);
+      memset(gp, 0, sizeof(float) * (size_t)tp);
+      orc_l2norm(qh, t, dk, q);
+      for (int64_t i = 0; i < (int64_t)t * dk; ++i) q[i] = q[i] * qscale + 0.0f;
+      orc_l2norm(kh, t, dk, k);
+      for (int i = 0; i < t; ++i) {
+        for (int e = 0; e < dv; ++e) vb[(int64_t)i * dv + e] = vh[(int64_t)i * dv + e] * bh[i];
+        for (int e = 0; e < dk; ++e) kb[(int64_t)i * dk + e] = k[(int64_t)i * dk + e] * bh[i];
+        gp[i] = gh[i];
       }
-    }
-    /* per chunk: pair, ut, intra, inverse, new values, k_cumdecay */
-    for (int c = 0; c < n; ++c) {
-      const float* cu = cum + c * C;
-      for (int i = 0; i < C; ++i)
-        for (int j = 0; j < C; ++j) pair[i * C + j] = j <= i ? expf(cu[i] - cu[j]) : 0.0f;
-      const float* kc = k + (int64_t)c * C * dk;
-      const float* kbc = kb + (int64_t)c * C * dk;
-      const float* qc = q + (int64_t)c * C * dk;
-      for (int i = 0; i < C; ++i)
-        for (int j = 0; j < C; ++j) {
-          float a = 0.0f, b = 0.0f;
-          for (int e = 0; e < dk; ++e) {
-            a += kbc[i * dk + e] * kc[j * dk + e];
-            b += qc[i * dk + e] * kc[j * dk + e];
+      for (int c = 0; c < n; ++c) {
+        float acc = 0.0f;
+        for (int i = 0; i < C; ++i) {
+          acc += gp[c * C + i];
+          cum[c * C + i] = acc;
+        }
+      }
+      /* per chunk: pair, ut, intra, inverse, new values, k_cumdecay */
+      for (int c = 0; c < n; ++c) {
+        const float* cu = cum + c * C;
+        for (int i = 0; i < C; ++i)
+          for (int j = 0; j < C; ++j) pair[i * C + j] = j <= i ? expf(cu[i] - cu[j]) : 0.0f;
+        const float* kc = k + (int64_t)c * C * dk;
+        const float* kbc = kb + (int64_t)c * C * dk;
+        const float* qc = q + (int64_t)c * C * dk;
+        for (int i = 0; i < C; ++i)
+          for (int j = 0; j < C; ++j) {
+            float a = 0.0f, b = 0.0f;
+            for (int e = 0; e < dk; ++e) {
+              a += kbc[i * dk + e] * kc[j * dk + e];
+              b += qc[i * dk + e] * kc[j * dk + e];
+            }
+            ut[i * C + j] = a * pair[i * C + j];
+            intra[(int64_t)c * C * C + i * C + j] = b * pair[i * C + j];
           }
-          ut[i * C + j] = a * pair[i * C + j];
-          intra[(int64_t)c * C * C + i * C + j] = b * pair[i * C + j];
+        orc_inv_unit_lower(ut, 1, C, inv);
+        mm(inv, vb + (int64_t)c * C * dv, nv + (int64_t)c * C * dv, C, C, dv);
+        for (int i = 0; i < C; ++i) {
+          float e = expf(cu[i]);
+          for (int x = 0; x < dk; ++x) dkb[i * dk + x] = kbc[i * dk + x] * e;
         }
-      orc_inv_unit_lower(ut, 1, C, inv);
-      mm(inv, vb + (int64_t)c * C * dv, nv + (int64_t)c * C * dv, C, C, dv);
-      for (int i = 0; i < C; ++i) {
-        float e = expf(cu[i]);
-        for (int x = 0; x < dk; ++x) dkb[i * dk + x] = kbc[i * dk + x] * e;
+        mm(inv, dkb, kcd + (int64_t)c * C * dk, C, C, dk);
       }
-      mm(inv, dkb, kcd + (int64_t)c * C * dk, C, C, dk);
-    }
-    /* state scan over chunks (:346-365) */
-    float* Sh = S;
-    if (s0)
-      memcpy(Sh, s0 + (int64_t)hh * dk * dv, sizeof(float) * (size_t)dk * dv);
-    else
-      memset(Sh, 0, sizeof(float) * (size_t)dk * dv);
-    for (int c = 0; c < n; ++c) {
-      const float* cu = cum + c * C;
-      float last = cu[C - 1];
-      /* v_new = new_values - k_cumdecay . S */
-      mm(kcd + (int64_t)c * C * dk, Sh, tmp, C, dk, dv);
-      for (int i = 0; i < C * dv; ++i) vnew[i] = nv[(int64_t)c * C * dv + i] - tmp[i];
-      /* inter = (q * e^cum) . S ; out = inter + intra . v_new */
-      for (int i = 0; i < C; ++i) {
-        float e = expf(cu[i]);
-        for (int j = 0; j < dv; ++j) {
-          float s = 0.0f;
-          for (int x = 0; x < dk; ++x) s += (q[((int64_t)c * C + i) * dk + x] * e) * Sh[x * dv + j];
-          float s2 = 0.0f;
-          for (int x = 0; x < C; ++x) s2 += intra[(int64_t)c * C * C + i * C + x] * vnew[x * dv + j];
-          int row = c * C + i;
-          if (row < t) out[((int64_t)hh * t + row) * dv + j] = s + s2;
+      /* state scan over chunks (:346-365) */
+      float* Sh = S;
+      if (s0)
+        memcpy(Sh, s0 + (int64_t)hh * dk * dv, sizeof(float) * (size_t)dk * dv);
+      else
+        memset(Sh, 0, sizeof(float) * (size_t)dk * dv);
+      for (int c = 0; c < n; ++c) {
+        const float* cu = cum + c * C;
+        float last = cu[C - 1];
+        /* v_new = new_values - k_cumdecay . S */
+        mm(kcd + (int64_t)c * C * dk, Sh, tmp, C, dk, dv);
+        for (int i = 0; i < C * dv; ++i) vnew[i] = nv[(int64_t)c * C * dv + i] - tmp[i];
+        /* inter = (q * e^cum) . S ; out = inter + intra . v_new */
+        for (int i = 0; i < C; ++i) {
+          float e = expf(cu[i]);
+          for (int j = 0; j < dv; ++j) {
+            float s = 0.0f;
+            for (int x = 0; x < dk; ++x) s += (q[((int64_t)c * C + i) * dk + x] * e) * Sh[x * dv + j];
+            float s2 = 0.0f;
+            for (int x = 0; x < C; ++x) s2 += intra[(int64_t)c * C * C + i * C + x] * vnew[x * dv + j];
+            int row = c * C + i;
+            if (row < t) out[((int64_t)hh * t + row) * dv + j] = s + s2;
+          }
         }
+        /* S = S * e^last + (k * e^(last - cum))^T . v_new */
+        float decay = mut_no_decay ? 1.0f : expf(last);
+        for (int i = 0; i < C; ++i) wdec[i] = expf(last - cu[i]);
+        for (int x = 0; x < dk; ++x)
+          for (int j = 0; j < dv; ++j) {
+            float s = 0.0f;
+            for (int i = 0; i < C; ++i) s += (k[((int64_t)c * C + i) * dk + x] * wdec[i]) * vnew[i * dv + j];
+            Sh[x * dv + j] = Sh[x * dv + j] * decay + s;
+          }
       }
-      /* S = S * e^last + (k * e^(last - cum))^T . v_new */
-      float decay = mut_no_decay ? 1.0f : expf(last);
-      for (int x = 0; x < dk; ++x)
-        for (int j = 0; j < dv; ++j) {
-          float s = 0.0f;
-          for (int i = 0; i < C; ++i) s += (k[((int64_t)c * C + i) * dk + x] * expf(last - cu[i])) * vnew[i * dv + j];
-          Sh[x * dv + j] = Sh[x * dv + j] * decay + s;
-        }
+      memcpy(s_out + (int64_t)hh * dk * dv, Sh, sizeof(float) * (size_t)dk * dv);
     }
-    memcpy(s_out + (int64_t)hh * dk * dv, Sh, sizeof(float) * (size_t)dk * dv);
+    free(q);
+    free(k);
+    free(vb);
+    free(kb);
+    free(gp);
+    free(cum);
+    free(pair);
+    free(ut);
+    free(intra);
+    free(inv);
+    free(nv);
+    free(kcd);
+    free(dkb);
+    free(S);
+    free(vnew);
+    free(tmp);
+    free(wdec);
   }
-  free(q);
-  free(k);
-  free(vb);
-  free(kb);
-  free(gp);
-  free(cum);
-  free(pair);
-  free(ut);
-  free(intra);
-  free(inv);
-  free(nv);
-  free(kcd);
-  free(dkb);
-  free(S);
-  free(vnew);
-  free(tmp);
 }
 
 /* The token-by-token gated delta recurrence that the reference checks its
@@ -284,7 +292,7 @@ void orc_gdn_recurrence(const float* qn, const float* kn, const float* v, const 
 }
 
 /* Depthwise causal conv over [tail || x] then SiLU, and the new tail
- * (qwen35.rs:419-431 with decoder.rs:137-151):
+ * (qwen35.rs:428-430 with decoder.rs:137-151):
  *   x (c, t) channel-major; tail (c, kw-1) or NULL (zeros); w (c, kw).
  *   y[c][i] = silu( sum_{u<kw} full[c][i+u] * w[c][u] ), full = [tail || x]
  *   new_tail = last kw-1 columns of full.
@@ -320,7 +328,7 @@ void orc_conv_silu(const float* x, const float* tail, const float* w, int c, int
   free(full);
 }
 
-/* Gated RMSNorm per head (qwen35.rs:443-449), f32 like the reference:
+/* Gated RMSNorm per head (qwen35.rs:447-451), f32 like the reference:
  *   y = core / sqrt(mean(core^2) + eps) * w * silu(z),  silu(z) = z / (1 + e^-z)
  * core, z: (rows, dv) f32 (z already cast from the model dtype); w: (dv).
  * bf16 != 0 rounds y to bf16 (the final .to_dtype(x.dtype())). */

@@ -3,7 +3,7 @@
 // input projections and out_proj.
 //
 //   conv:  depthwise causal conv over [conv state || x] + SiLU, new state
-//          (qwen35.rs:424-428, decoder.rs:137-151), model dtype ops;
+//          (qwen35.rs:428-430, decoder.rs:137-151), model dtype ops;
 //   prep:  per (row, value head, 64-token chunk), in f32: q, k l2norm
 //          (q * dk^-0.5), beta = sigmoid(b), g = softplus(a + dt_bias) * -e^A,
 //          cum = prefix sum of g, ut = (k beta) k^T * pair, intra = q k^T * pair,
@@ -13,7 +13,7 @@
 //          state split into 16-column slices (columns of S evolve
 //          independently), one workgroup per (row, head, slice);
 //   norm:  gated RMSNorm * SiLU(z) and the cast to the model dtype
-//          (qwen35.rs:443-449).
+//          (qwen35.rs:447-451).
 //
 // All chunk-rule products run on v_mfma_f32_16x16x4_f32 (full f32 like the
 // reference).  Lane layout (16x16x4): A lane l holds A[l%16][l/16], B lane l
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs g) {
   }
 }
 
-// New conv state: the last K-1 columns of [state || x] (qwen35.rs:425).
+// New conv state: the last K-1 columns of [state || x] (qwen35.rs:429).
 template <typename T>
 __global__ __launch_bounds__(256) void gdn_conv_state_kernel(GdnArgs g) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   const int c = blockIdx.x % g.n_chunks;
   const int hr = blockIdx.x / g.n_chunks;
   const int h = hr % g.nv, r = hr / g.nv;
-  const int kh = h / (g.nv / g.nk);  // value head h reads key head h / (nv/nk) (qwen35.rs:433-437)
+  const int kh = h / (g.nv / g.nk);  // value head h reads key head h / (nv/nk) (qwen35.rs:436-442)
   const int key_dim = g.nk * kD;
   const int t0 = c * kC;
 
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
 
 // ---------------------------------------------------------------------------
 // norm: one wave per (row, token, value head): y = core / sqrt(mean core^2
-// + eps) * w * silu(z), cast to the model dtype (qwen35.rs:443-449).
+// + eps) * w * silu(z), cast to the model dtype (qwen35.rs:447-451).
 template <typename T>
 __global__ __launch_bounds__(256) void gdn_norm_kernel(GdnArgs g) {
   const int lane = threadIdx.x & 63;

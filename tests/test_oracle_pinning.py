@@ -397,4 +397,93 @@ def test_inv_unit_lower_matches_definition(orc):
 
 def test_softplus_closed_form(orc):
     for x in (-30.0, -2.0, 0.0, 0.5, 3.0, 40.0):
-        assert abs(orc.softplus(x) - math.log1p(math.exp(x)) if x < 30 else abs(orc.softplus(x) - x)) < 1e-5
+        want = math.log1p(math.exp(x)) if x < 30 else x
+        assert abs(orc.softplus(x) - want) <= 1e-5 * max(1.0, abs(want))
+
+
+def test_l2norm_unit_rows_and_direction(orc):
+    x = RNG.standard_normal((50, 128)).astype(np.float32) * 3.0
+    y = orc.l2norm(x)
+    assert np.abs(np.linalg.norm(y.astype(np.float64), axis=1) - 1.0).max() < 1e-5
+    assert np.abs(y * np.linalg.norm(x.astype(np.float64), axis=1, keepdims=True) - x).max() < 1e-4
+    # the 1e-6 inside the root (qwen35.rs:252): a zero row stays zero, a tiny row is damped
+    z = orc.l2norm(np.zeros((1, 8), np.float32))
+    assert np.all(z == 0.0)
+
+
+def _conv_direct(x, tail, w):
+    """Depthwise causal conv + SiLU in f64 by the definition: y[c, i] =
+    silu(sum_u full[c, i + u] w[c, u]) over full = [tail || x]."""
+    c, t = x.shape
+    kw = w.shape[1]
+    full = np.concatenate([np.zeros((c, kw - 1)) if tail is None else tail, x], 1).astype(np.float64)
+    y = np.zeros((c, t))
+    for i in range(t):
+        y[:, i] = (full[:, i:i + kw] * w).sum(1)
+    return y / (1.0 + np.exp(-y)), full[:, t:t + kw - 1]
+
+
+def test_conv_silu_f32_matches_direct_convolution(orc):
+    c, t, kw = 6, 11, 4
+    x = RNG.standard_normal((c, t)).astype(np.float32)
+    tail = RNG.standard_normal((c, kw - 1)).astype(np.float32)
+    # taps differ in size and sign, so a reversed or shifted kernel fails
+    w = (np.array([0.1, -0.7, 0.4, 1.3], np.float32)[None, :] * (1.0 + np.arange(c, dtype=np.float32)[:, None] / 4)).astype(np.float32)
+    for tl in (None, tail):
+        y, nt = orc.conv_silu(x, tl, w, False)
+        ry, rnt = _conv_direct(x, tl, w)
+        assert np.abs(y - ry).max() < 1e-5
+        assert np.array_equal(nt, rnt.astype(np.float32))
+    # a short call: the new tail still reaches back into the old one
+    y, nt = orc.conv_silu(x[:, :2], tail, w, False)
+    ry, rnt = _conv_direct(x[:, :2], tail, w)
+    assert np.abs(y - ry).max() < 1e-5 and np.array_equal(nt, rnt.astype(np.float32))
+
+
+def test_conv_silu_bf16_within_rounding_of_exact(orc):
+    c, t, kw = 16, 40, 4
+    x = orc.round_bf16(RNG.standard_normal((c, t)).astype(np.float32))
+    w = orc.round_bf16((RNG.standard_normal((c, kw)) * 0.5).astype(np.float32))
+    y, _ = orc.conv_silu(x, None, w, True)
+    ry, _ = _conv_direct(x, None, w)
+    assert np.array_equal(y, orc.round_bf16(y))  # every output is a bf16 value
+    assert np.abs(y - ry).max() <= 2e-2 * max(1.0, np.abs(ry).max())
+
+
+def test_gated_rmsnorm_closed_form(orc):
+    rows, dv = 40, 128
+    core = RNG.standard_normal((rows, dv)).astype(np.float32)
+    z = RNG.standard_normal((rows, dv)).astype(np.float32)
+    w = (1.0 + 0.1 * RNG.standard_normal(dv)).astype(np.float32)
+    y = orc.gated_rmsnorm(core, z, w, 1e-6, False)
+    c64 = core.astype(np.float64)
+    ref = c64 / np.sqrt((c64 ** 2).mean(1, keepdims=True) + 1e-6) * w * (z / (1.0 + np.exp(-z.astype(np.float64))))
+    assert np.abs(y - ref).max() < 1e-5
+    yb = orc.gated_rmsnorm(core, z, w, 1e-6, True)
+    assert np.array_equal(yb, orc.round_bf16(yb)) and np.abs(yb - ref).max() < 2e-2 * np.abs(ref).max()
+
+
+def test_gdn_layer_value_heads_follow_key_heads_in_blocks(orc):
+    """Value head h reads key head h // (nv / nk) (the unsqueeze(2).expand of
+    qwen35.rs:438).  Swapping the two key heads' q/k channels must swap
+    value heads {0, 1} with {2, 3} and nothing else."""
+    from cev_hip import configs
+    nk, nv, dk, dv = 2, 4, 8, 8
+    w = configs.GdnWorkload("rep", 3, False, 1, 20, nk=nk, nv=nv, dk=dk, dv=dv)
+    inp = w.inputs()
+    args = lambda m, z, b, a: orc.gdn_layer(m, z, b, a, inp["conv_w_p"], inp["neg_a"], inp["dt_bias"], inp["norm_w"], nk, nv,
+                                            dk, dv, w.eps, False)[0]
+    kd = nk * dk
+    perm_c = np.concatenate([np.arange(dk, 2 * dk), np.arange(dk), kd + np.arange(dk, 2 * dk), kd + np.arange(dk),
+                             2 * kd + np.arange(2 * dv, 4 * dv), 2 * kd + np.arange(2 * dv)])
+    perm_h = np.array([2, 3, 0, 1])
+    # conv weights must follow the channels for the swap to be a symmetry
+    inp["conv_w_p"] = inp["conv_w"]
+    y = args(inp["mixed"], inp["z"], inp["b"], inp["a"])
+    inp["conv_w_p"] = inp["conv_w"][perm_c]
+    zz = inp["z"].reshape(1, w.t, nv, dv)[:, :, perm_h].reshape(1, w.t, nv * dv)
+    yp = args(inp["mixed"][:, :, perm_c], zz, inp["b"][:, :, perm_h], inp["a"][:, :, perm_h])
+    want = y.reshape(1, w.t, nv, dv)[:, :, perm_h].reshape(1, w.t, nv * dv)
+    assert np.abs(yp - want).max() < 1e-5
+    # the tiled order (h % nk) would pair value head 1 with key head 1: not a symmetry of the layer
+    assert np.abs(y.reshape(1, w.t, nv, dv)[:, :, 0] - y.reshape(1, w.t, nv, dv)[:, :, 2]).max() > 1e-3
