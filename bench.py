@@ -156,6 +156,20 @@ def roofline(flops: float, alg: int, ms: float, dtype: str, kernel: str, traffic
     return roof
 
 
+def capture(fns):
+    """One HIP graph per callable: every kernel the callable launches on the
+    current stream is recorded once and replayed without host work."""
+    import torch
+    graphs = []
+    for f in fns:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            f()
+        graphs.append(g)
+    torch.cuda.synchronize()
+    return graphs
+
+
 def calibrate_gemm(n: int, steps: int, warmup: int):
     """The practical bf16 MFMA ceiling on this card: hipBLASLt's n^3 GEMM
     (torch.matmul) on random N(0,1) operands and on all-zero operands.  The
@@ -204,14 +218,23 @@ def bench_gdn(args, w, dev):
     y = torch.empty((w.batch, w.t, w.nv * w.dv), dtype=mdt, device=dev)
     conv_out = torch.empty((w.batch, w.conv_dim, w.kernel - 1), dtype=mdt, device=dev)
     s_out = torch.empty((w.batch, w.nv, w.dk, w.dv), dtype=torch.float32, device=dev)
-    for _ in range(args.warmup):
+    def fwd():
         layer(*xs, s_in=s_in, y=y, conv_out=conv_out, s_out=s_out)
+
+    for _ in range(args.warmup):
+        fwd()
+    torch.cuda.synchronize()
+    if args.graph:
+        (g,) = capture([fwd])
+        fwd = g.replay
+        for _ in range(args.warmup):
+            fwd()
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     t0 = time.perf_counter()
     for a, b in ev:
         a.record()
-        layer(*xs, s_in=s_in, y=y, conv_out=conv_out, s_out=s_out)
+        fwd()
         b.record()
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
@@ -230,7 +253,8 @@ def bench_gdn(args, w, dev):
         "data": "synthetic (seeded projection outputs; beta uniform in (0,1), decay log-uniform in [1e-3, 1])",
         "config": {"workload": f"{w.name}: Gated DeltaNet layer, batch {w.batch} x {w.t} tokens, Hk={w.nk} Hv={w.nv} "
                                f"dk={w.dk} dv={w.dv}, conv kernel {w.kernel}, 64-token chunks, "
-                               f"{'bf16' if w.bf16 else 'f32'} inputs, f32 chunk rule"},
+                               f"{'bf16' if w.bf16 else 'f32'} inputs, f32 chunk rule",
+                   "launch": "hip graph replay" if args.graph else "direct launches"},
         "roofline": roofline(w.flops(), alg, layer_ms, "f32", "gdn conv + prep + scan + norm (one forward call)", None),
         "device": device_info().name,
     }
@@ -248,6 +272,8 @@ def main():
                     help="c3 (default): the 32k-prefix packed-prefill attention; c5gdn / c5gdnrows: the Gated DeltaNet "
                          "layer core over one 4096-token row / 32 rows of 64 tokens")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline leg")
+    ap.add_argument("--graph", type=int, default=0,
+                    help="1: capture each timed call once in a HIP graph and replay it; 0 (default): launch directly (graph launch costs more than it saves here)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the workload, run `steps` device copies of MIB MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes)")
@@ -289,15 +315,22 @@ def main():
     for _ in range(args.warmup):
         layer.forward()
     torch.cuda.synchronize()
+    k1, k2 = layer.qknorm, layer.attend
+    if args.graph:
+        g1, g2 = capture([k1, k2])
+        k1, k2 = g1.replay, g2.replay
+        for _ in range(args.warmup):
+            k1()
+            k2()
 
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         ev[i][0].record()
-        layer.qknorm()
+        k1()
         ev[i][1].record()
-        layer.attend()
+        k2()
         ev[i][2].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -328,6 +361,7 @@ def main():
             "hq": w.hq, "hkv": w.hkv, "head_dim": w.d, "prefix": w.prefix,
             "suffix_blocks": len(w.blocks), "block_len": w.blocks[0], "query_tokens": w.t,
             "causal": w.causal, "gated": w.gated,
+            "launch": "hip graph replay (K1 and K2 each one graph)" if args.graph else "direct launches",
         },
         "tflops": flops / (ms_step * 1e-3) / 1e12,
         "k1_ms": k1_ms,

@@ -406,6 +406,10 @@ constexpr int kVBase = kBuf * kTileBytes;  // K tiles first, then V tiles
 __device__ __forceinline__ int k_slot(int blk, int row) { return blk ^ (row & 15); }
 __device__ __forceinline__ int v_slot(int blk, int row) { return blk ^ ((row & 3) << 2); }
 
+// Workgroup barrier after this wave's LDS operations have completed; global
+// loads may still be in flight.  The asm is a compiler memory barrier too.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -636,9 +640,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
     };
 
     // Stale LDS must hold finite values: a masked key's V row is multiplied
-    // by p = 0.  Zero every buffer once before the first fetch.
+    // by p = 0.  Zero every buffer once before the first fetch.  The
+    // barrier waits for LDS writes only, so the query loads stay in flight
+    // under the first fetches (__syncthreads would drain them first).
     for (int i = tid; i < 2 * kBuf * kTileBytes / 16; i += kAttnWaves * 64) *(f32x4*)(lds + 16 * i) = f32x4{};
-    __syncthreads();
+    lds_barrier();
 
     // chs[k] is chunk i + k of the part; chunks past its end are empty
     // (their fetch reads no memory).
@@ -1018,9 +1024,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
 
 // Combines the parts of split tiles: for each (row, head),
 //   M = max_s m_s,  L = sum_s 2^(m_s - M) l_s,  O = sum_s 2^(m_s - M) O_s / L.
-// One wave per (row, head), kMergeWaves per workgroup; lanes first reduce
-// the parts' (m, l) across the wave, then each lane accumulates its
-// head-dim slice over the parts with independent loads.
+// One wave per (row, head), kMergeWaves per workgroup.  Lane l reads the
+// four head-dim columns 4 (l % (D/4)) .. of every (64 / (D/4))-th part
+// starting at part l / (D/4); a batch of NB parts per lane is loaded before
+// any of it is used, so a batch costs one memory latency, and batches
+// combine with an online rescale.  The launcher picks NB from the part
+// count (fewer registers, more waves per SIMD for few parts).
 constexpr int kMergeWaves = 4;
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -1029,17 +1038,12 @@ __device__ __forceinline__ float wave_max(float x) {
   return x;
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-  return x;
-}
-
-template <typename T, int D>
+template <typename T, int D, int NB>
 __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a) {
   constexpr bool BF = sizeof(T) == 2;
-  constexpr int EPL = D / 64;  // head-dim values per lane
-  __shared__ float wsh[kMergeWaves][kSplitMax];
+  constexpr int Q = D / 4;    // 4-column groups of a record
+  constexpr int PS = 64 / Q;  // parts read side by side: 2 at d = 128, 1 at d = 256
+  static_assert(Q * PS == 64, "one wave covers the head dim");
   if (!plan_ok(a)) return;
   const cev_plan_header* ph = (const cev_plan_header*)a.plan;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1055,48 +1059,62 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
   const int row = td.x + r;
   const int64_t pf = cev_attn_partial_floats(D);
   const int S = a.n_splits;
+  const int col = lane % Q, phase = lane / Q;
   const float* rec = a.ws + ((int64_t)row * a.hq + head) * S * pf;
-  float M = -INFINITY;
-  for (int s = lane; s < S; s += 64) M = fmaxf(M, rec[s * pf + D]);
-  M = wave_max(M);
-  float L = 0.0f;
-  for (int s = lane; s < S; s += 64) {
-    const float w = fast_exp2(rec[s * pf + D] - M);
-    wsh[wave][s] = w;
-    L += w * rec[s * pf + D + 1];
-  }
-  L = wave_sum(L);
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  float acc[EPL];
+
+  // Every record holds a finite m (a part with no visible key keeps its
+  // initial -1e30 and l = 0), so M is finite after the first batch.
+  float M = -INFINITY, L = 0.0f;
+  f32x4 acc = {};
+  for (int s0 = 0; s0 < S; s0 += PS * NB) {
+    f32x4 o[NB];
+    float2 ml[NB];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.0f;
-  const float* base = rec + lane * EPL;
-#pragma unroll 4
-  for (int s = 0; s < S; ++s) {
-    const float w = wsh[wave][s];
-    float v[EPL];
-    if constexpr (EPL == 2) {
-      const float2 x = *(const float2*)(base + s * pf);
-      v[0] = x.x;
-      v[1] = x.y;
-    } else {
-      const f32x4 x = *(const f32x4*)(base + s * pf);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) v[e] = x[e];
+    for (int i = 0; i < NB; ++i) {
+      const int s = s0 + PS * i + phase;
+      if (s < S) {
+        o[i] = *(const f32x4*)(rec + s * pf + 4 * col);
+        ml[i] = *(const float2*)(rec + s * pf + D);
+      } else {
+        o[i] = f32x4{};
+        ml[i] = make_float2(-INFINITY, 0.0f);
+      }
     }
+    float mb = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += w * v[e];
+    for (int i = 0; i < NB; ++i) mb = fmaxf(mb, ml[i].x);
+    const float m_new = fmaxf(M, wave_max(mb));
+    const float alpha = fast_exp2(M - m_new);
+    acc *= alpha;
+    L *= alpha;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const float w = fast_exp2(ml[i].x - m_new);
+      acc += w * o[i];
+      L += w * ml[i].y;
+    }
+    M = m_new;
+  }
+  if constexpr (PS == 2) {
+    // the two part phases of one column group sit 32 lanes apart
+    L += __shfl_xor(L, 32, 64);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], 32, 64);
+    if (phase != 0) return;
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh + lane * EPL;
-  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh + lane * EPL : nullptr;
+  const int d = 4 * col;
+  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh + d;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh + d : nullptr;
+  float v[4], gv[4];
+  if (gp) load_vec4<T>(gp, gv);
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
+  for (int e = 0; e < 4; ++e) {
     float x = BF ? acc[e] * inv : (L > 0.0f ? acc[e] / L : 0.0f);
-    if (gp) x = gate_value(x, (float)gp[e], BF);
-    op[e] = (T)x;
+    if (gp) x = gate_value(x, gv[e], BF);
+    v[e] = x;
   }
+  store_vec4<T>(op, v);
 }
 
 template <typename T, int D>
@@ -1113,7 +1131,15 @@ int32_t launch(const AttnArgs& a, hipStream_t stream) {
     const int groups = (a.tile_rows + kMergeWaves - 1) / kMergeWaves;
     const int64_t mgrid = (int64_t)a.n_tiles * groups * a.hq;
     if (mgrid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "merge grid too large");
-    hipLaunchKernelGGL((attn_merge_kernel<T, D>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
+    const int per_lane = (a.n_splits + 64 / (D / 4) - 1) / (64 / (D / 4));  // parts each lane reads
+    if (per_lane <= 2)
+      hipLaunchKernelGGL((attn_merge_kernel<T, D, 2>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
+    else if (per_lane <= 4)
+      hipLaunchKernelGGL((attn_merge_kernel<T, D, 4>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
+    else if (per_lane <= 8)
+      hipLaunchKernelGGL((attn_merge_kernel<T, D, 8>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_merge_kernel<T, D, 16>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
     e = hipGetLastError();
     if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "attention merge launch: %s", hipGetErrorString(e));
   }

@@ -14,10 +14,16 @@
 // rounded HIP forms (hipcc's default); __fsqrt_rn is not (it maps to the
 // native approximate square root) and must not be used here.
 //
-// Work split: a wave normalises 8 vectors (token, head) at a time.  Lanes
-// load the 8 x D elements coalesced, the squares go through LDS and lanes
-// 0..7 each sum one vector in element order, so the sum matches the
-// reference's sequential f32 sum bit for bit.
+// Two work splits, both summing each vector's squares in element order so
+// the sum matches the reference's sequential f32 sum bit for bit:
+//   qknorm_rope_lane_kernel (full rotary or a quarter of it, 16-byte aligned
+//     rows): one lane per vector (token, head).  The lane loads its vector
+//     in 16-byte chunks into registers, sums, normalises and rotates the
+//     pairs (i, i + rot/2) there and stores 16-byte chunks: no LDS, no
+//     barrier, one dependent add chain of D per lane.
+//   qknorm_rope_kernel (any other shape): a wave normalises 8 vectors at a
+//     time; lanes load coalesced, the squares go through LDS and lanes 0..7
+//     each sum one vector.
 #include "cev_device.h"
 #include "cev_internal.h"
 
@@ -157,12 +163,249 @@ __global__ __launch_bounds__(WAVES * 64) void qknorm_rope_kernel(QkArgs a) {
   }
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Element j of a 16-byte chunk: bf16 packs two per dword (low half first).
+template <typename T>
+__device__ __forceinline__ float chunk_get(const u32x4& c, int j) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t w = c[j >> 1];
+    return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    return __uint_as_float(c[j]);
+  }
+}
+// Elements 2i, 2i+1 of a chunk from two values: bf16 rounds both to nearest
+// even and packs them (one v_cvt_pk_bf16_f32); f32 stores them as they are.
+template <typename T>
+__device__ __forceinline__ void chunk_set2(u32x4& c, int i, float lo, float hi) {
+  if constexpr (sizeof(T) == 2) {
+    const __bf16 l = (__bf16)lo, h = (__bf16)hi;
+    c[i] = (uint32_t)__builtin_bit_cast(uint16_t, l) | ((uint32_t)__builtin_bit_cast(uint16_t, h) << 16);
+  } else {
+    c[2 * i] = __float_as_uint(lo);
+    c[2 * i + 1] = __float_as_uint(hi);
+  }
+}
+
+constexpr int kLaneThreads = 256;
+
+// Waves per SIMD the register budget is held to: the packed vector takes
+// D * sizeof(T) / 16 * 4 registers per lane.
+template <typename T, int D>
+constexpr int lane_waves() { return D * (int)sizeof(T) >= 512 ? 3 : 4; }
+
+template <typename T, int D, int ROT>
+__global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(lane_waves<T, D>()))) void qknorm_rope_lane_kernel(
+    QkArgs a) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int VEC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  constexpr int NC = D / VEC;               // chunks per vector
+  constexpr int HALF = ROT / 2;
+  constexpr int HC = HALF / VEC;            // chunks in the first rotary half
+  static_assert(HALF % VEC == 0 && ROT <= D, "rotary halves are whole chunks");
+  auto rnd = [](float x) { return BF ? bf16_round(x) : x; };
+  // The weights as the norm multiplies them (1 + w rounded to the dtype
+  // for the zero-centred form), once per workgroup: q's then k's.
+  __shared__ __align__(16) float weff[2][D];
+  for (int i = threadIdx.x; i < 2 * D; i += kLaneThreads) {
+    const T* wsrc = i < D ? (const T*)a.w_q : (const T*)a.w_k;
+    const bool have = i < D ? a.hq > 0 : a.hkv > 0;
+    float w = 0.0f;
+    if (have) {
+      if constexpr (BF)
+        w = bf16_from_bits(((const uint16_t*)wsrc)[i % D]);
+      else
+        w = ((const float*)wsrc)[i % D];
+      if (a.plus_one) w = rnd(w + 1.0f);
+    }
+    weff[i / D][i % D] = w;
+  }
+  __syncthreads();
+
+  const int64_t nq = (int64_t)a.t * a.hq;
+  const int64_t total = nq + (int64_t)a.t * a.hkv;
+  const int64_t v = (int64_t)blockIdx.x * kLaneThreads + threadIdx.x;
+  if (v >= total) return;
+  const T* src;
+  T* dst;
+  int tk;
+  const bool is_q = v < nq;
+  if (is_q) {
+    tk = (int)(v / a.hq);
+    const int h = (int)(v % a.hq);
+    src = (const T*)a.q_in + tk * a.qi_st + h * a.qi_sh;
+    dst = (T*)a.q_out + tk * a.qo_st + h * a.qo_sh;
+  } else {
+    const int64_t vk = v - nq;
+    tk = (int)(vk / a.hkv);
+    const int h = (int)(vk % a.hkv);
+    src = (const T*)a.k_in + tk * a.ki_st + h * a.ki_sh;
+    dst = (T*)a.k_out + tk * a.ko_st + h * a.ko_sh;
+  }
+  const float* wl = weff[is_q ? 0 : 1];
+  u32x4 c[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) c[k] = *(const u32x4*)(src + k * VEC);
+  const int p = a.pos[tk];
+
+  float sum2 = 0.0f;
+  int min_exp = 0;  // smallest frexp exponent of a nonzero element (0 for 0)
+#pragma unroll
+  for (int k = 0; k < NC; ++k)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float x = chunk_get<T>(c[k], j);
+      sum2 += x * x;
+      min_exp = min(min_exp, __builtin_amdgcn_frexp_expf(x));
+    }
+  const float m = rnd(sqrtf(sum2 / (float)D + a.eps));
+  // x / m, correctly rounded, for every element.  With y = RN(1/m),
+  // q0 = RN(x y) and the exact residual r = x - q0 m, RN(q0 + r y) is the
+  // correctly rounded quotient (Markstein) as long as r cannot underflow or
+  // overflow: every nonzero |x| in [2^-96, 2^60] (sum2 <= 2^120 bounds the
+  // top) and m in [2^-20, 2^20], checked for the whole wave; otherwise the
+  // wave takes the IEEE division.  copysign keeps the sign of -0 / m.
+  const bool fast = min_exp >= -95 && sum2 <= 0x1p120f && m >= 0x1p-20f && m <= 0x1p20f;
+  const float y = 1.0f / m;
+  const bool p_ok = p >= 0 && p < a.n_pos;
+  const T* crow = (const T*)a.cos_t + (int64_t)(p_ok ? p : 0) * HALF;
+  const T* srow = (const T*)a.sin_t + (int64_t)(p_ok ? p : 0) * HALF;
+
+  // The chunks pass through an empty asm so the compiler unpacks them again
+  // below instead of keeping all D unpacked values of the sum live.
+#pragma unroll
+  for (int k = 0; k < NC; ++k) asm volatile("" : "+v"(c[k]));
+
+  // y = dtype(dtype(x / m) * w) on chunk k, then rotate-half on the pairs
+  // (i, i + ROT/2) of the first ROT elements; a position outside the table
+  // yields NaN there instead of a stray read.
+  auto pair = [&](auto fast_c, u32x4& c0, u32x4& c1, int k) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    auto quot = [&](float x) {
+      if constexpr (FAST) {
+        const float q0 = x * y;
+        const float r = __builtin_fmaf(-q0, m, x);
+        return __builtin_copysignf(__builtin_fmaf(r, y, q0), q0);
+      } else {
+        return x / m;
+      }
+    };
+    const u32x4 cc = *(const u32x4*)(crow + k * VEC);
+    const u32x4 sc = *(const u32x4*)(srow + k * VEC);
+    float r0[VEC], r1[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const f32x4 w0 = *(const f32x4*)(wl + k * VEC + (j & ~3));
+      const f32x4 w1 = *(const f32x4*)(wl + (k + HC) * VEC + (j & ~3));
+      const float y0 = rnd(rnd(quot(chunk_get<T>(c0, j))) * w0[j & 3]);
+      const float y1 = rnd(rnd(quot(chunk_get<T>(c1, j))) * w1[j & 3]);
+      const float co = p_ok ? chunk_get<T>(cc, j) : __builtin_nanf("");
+      const float si = p_ok ? chunk_get<T>(sc, j) : __builtin_nanf("");
+      r0[j] = rnd(y0 * co) - rnd(y1 * si);
+      r1[j] = rnd(y0 * si) + rnd(y1 * co);
+    }
+#pragma unroll
+    for (int i = 0; i < VEC / 2; ++i) {
+      chunk_set2<T>(c0, i, r0[2 * i], r0[2 * i + 1]);
+      chunk_set2<T>(c1, i, r1[2 * i], r1[2 * i + 1]);
+    }
+  };
+  auto single = [&](auto fast_c, u32x4& c0, int k) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    float yv[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float x = chunk_get<T>(c0, j);
+      float q;
+      if constexpr (FAST) {
+        const float q0 = x * y;
+        q = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, m, x), y, q0), q0);
+      } else {
+        q = x / m;
+      }
+      yv[j] = rnd(rnd(q) * (*(const f32x4*)(wl + k * VEC + (j & ~3)))[j & 3]);
+    }
+#pragma unroll
+    for (int i = 0; i < VEC / 2; ++i) chunk_set2<T>(c0, i, yv[2 * i], yv[2 * i + 1]);
+  };
+
+  if (__all(fast)) {
+#pragma unroll
+    for (int k = 0; k < HC; ++k) {
+      pair(std::true_type{}, c[k], c[k + HC], k);
+      // keeps each chunk's weight and table reads next to their use
+      // (hoisted, they take a register each and cap the waves per SIMD)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int k = 2 * HC; k < NC; ++k) {
+      single(std::true_type{}, c[k], k);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int k = 0; k < NC; ++k) *(u32x4*)(dst + k * VEC) = c[k];
+  } else {
+    // Rare (a wave with a tiny, huge or non-finite element): IEEE division,
+    // one chunk or rotary pair at a time, re-read from the input (each
+    // chunk is read before its own store, so q_out may alias q_in).
+#pragma unroll 1
+    for (int k = 0; k < HC; ++k) {
+      u32x4 c0 = *(const u32x4*)(src + k * VEC), c1 = *(const u32x4*)(src + (k + HC) * VEC);
+      pair(std::false_type{}, c0, c1, k);
+      *(u32x4*)(dst + k * VEC) = c0;
+      *(u32x4*)(dst + (k + HC) * VEC) = c1;
+    }
+#pragma unroll 1
+    for (int k = 2 * HC; k < NC; ++k) {
+      u32x4 c0 = *(const u32x4*)(src + k * VEC);
+      single(std::false_type{}, c0, k);
+      *(u32x4*)(dst + k * VEC) = c0;
+    }
+  }
+}
+
+
+// The one-lane-per-vector kernel covers full and quarter rotary when every
+// row, weight vector and table row is a whole number of 16-byte chunks.
+template <typename T>
+bool lane_kernel_fits(const QkArgs& a, int d) {
+  const int vec = 16 / (int)sizeof(T);
+  auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const int64_t st[] = {a.qi_st, a.qi_sh, a.ki_st, a.ki_sh, a.qo_st, a.qo_sh, a.ko_st, a.ko_sh};
+  for (int64_t x : st)
+    if (x % vec) return false;
+  if (!(al(a.cos_t) && al(a.sin_t))) return false;
+  if (a.hq && !(al(a.q_in) && al(a.q_out) && al(a.w_q))) return false;
+  if (a.hkv && !(al(a.k_in) && al(a.k_out) && al(a.w_k))) return false;
+  if (sizeof(T) == 4 && d == 256) return false;  // 256 registers of f32 per vector
+  return a.rot == d || a.rot == d / 4;
+}
+
 template <typename T>
 int32_t launch_qk(const QkArgs& a, int d, hipStream_t s) {
   const int64_t vecs = (int64_t)a.t * (a.hq + a.hkv);
+  if (vecs == 0) return CEV_OK;
+  if (lane_kernel_fits<T>(a, d)) {
+    const int64_t grid = (vecs + kLaneThreads - 1) / kLaneThreads;
+    if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm grid too large");
+    const dim3 g((unsigned)grid), b(kLaneThreads);
+    if (d == 128 && a.rot == 128)
+      hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 128, 128>), g, b, 0, s, a);
+    else if (d == 128)
+      hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 128, 32>), g, b, 0, s, a);
+    else if constexpr (sizeof(T) == 2) {
+      if (a.rot == 256)
+        hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 256, 256>), g, b, 0, s, a);
+      else
+        hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 256, 64>), g, b, 0, s, a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "qknorm_rope launch: %s", hipGetErrorString(e));
+    return CEV_OK;
+  }
   const int64_t per_wg = (int64_t)WAVES * VPW;
   const int64_t grid = (vecs + per_wg - 1) / per_wg;
-  if (grid == 0) return CEV_OK;
   if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm grid too large");
   if (d == 128)
     hipLaunchKernelGGL((qknorm_rope_kernel<T, 128>), dim3((unsigned)grid), dim3(WAVES * 64), 0, s, a);

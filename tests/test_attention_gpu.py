@@ -257,3 +257,90 @@ def test_split_gated_rows(gpu, orc):
     ol = OracleLayer(orc, w, gl.np_inputs)
     gl.forward()
     _check_blocks(gl, ol, [3, 17], BF16_TOL)
+
+
+@pytest.mark.parametrize("name", ["c1", "hbm", "c5a"])
+def test_graph_replay_matches_eager(gpu, name):
+    """K1 + K2 captured once in a HIP graph: every replay, with eager work and
+    synchronisations between replays, gives the eager result bit for bit
+    (split plans included: the merge pass is part of the graph)."""
+    import torch
+    w = configs.WORKLOADS[name]()
+    table = cev_hip.BlockTable.from_rows(len(w.blocks), w.blocks[0], w.prefix, causal=True) if name == "c5a" else None
+    gl = GpuLayer(w, gpu, table=table)
+    _say(f"test graph replay {w.name}: n_splits={gl.attn.plan.n_splits}")
+    gl.forward()
+    torch.cuda.synchronize()
+    want = to_np(gl.out).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gl.qknorm()
+        gl.attend()
+    for i in range(3):
+        gl.out.fill_(float("nan"))
+        gl.q.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(to_np(gl.out), want), f"replay {i}"
+
+
+def _same_bits(a, b):
+    """Bit equality of two f32 arrays (so -0 != +0), NaN matching NaN."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | (a.view(np.uint32) == b.view(np.uint32))))
+
+
+@pytest.mark.parametrize("bf16,d,rot,plus_one,inplace", [(True, 128, 128, False, False), (True, 256, 64, True, False),
+                                                         (False, 128, 128, False, False), (True, 128, 128, False, True)])
+def test_qknorm_rope_bit_exact_on_extreme_values(gpu, orc, bf16, d, rot, plus_one, inplace):
+    """One lane normalises one vector; a wave whose vectors are all in the
+    fast division's range divides by reciprocal + FMA correction, any other
+    wave uses IEEE division.  Vectors with zeros, -0, elements below 2^-96,
+    huge elements and ordinary ones (both kinds of waves, and waves that
+    mix them) must all match the oracle bit for bit, the sign of zero
+    included; the in-place form (q_out = q_in) too."""
+    import torch
+    from cev_hip import synth
+    t, hq, hkv, eps, theta = 96, 4, 2, 1e-6, 1e6
+    dt = torch.bfloat16 if bf16 else torch.float32
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((t, hq, d)).astype(np.float32)
+    k = rng.standard_normal((t, hkv, d)).astype(np.float32)
+    # tokens 0..15 (first wave of q): ordinary; 16..31: a tiny element in
+    # some vectors; 32..47: zero and -0 vectors; 48..63: huge elements;
+    # 64..95: scattered -0 and tiny elements in k
+    q[16:32:3, 1, 5] = 2.0 ** -100
+    q[17:32:5, 2, 70] = -(2.0 ** -110)
+    q[32:40] = 0.0
+    q[40:48] = -0.0
+    q[48:64:4, 0, 3] = 2.0 ** 70
+    q[50, 3, 9] = 2.0 ** 66
+    k[64:96:2, 0, ::7] = -0.0
+    k[65:96:4, 1, 11] = 2.0 ** -98
+    if bf16:
+        q, k = synth.round_bf16(q), synth.round_bf16(k)
+    wq = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32) - (1.0 if plus_one else 0.0)
+    wk = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32) - (1.0 if plus_one else 0.0)
+    if bf16:
+        wq, wk = synth.round_bf16(wq), synth.round_bf16(wk)
+    pos = (np.arange(t) % 40 + 3).astype(np.int32)
+    n_pos = 64
+    rotary = cev_hip.Rotary(theta, rot, n_pos, dt, gpu)
+    dq, dk = to_dev(q, bf16, gpu), to_dev(k, bf16, gpu)
+    kw = dict(q_out=dq, k_out=dk) if inplace else {}
+    qo, ko = cev_hip.qknorm_rope(dq, dk, to_dev(wq, bf16, gpu), to_dev(wk, bf16, gpu), torch.from_numpy(pos).to(gpu), rotary, eps,
+                                 plus_one=plus_one, **kw)
+    torch.cuda.synchronize()
+    cos, sin = orc.rope_table(theta, rot, n_pos, bf16)
+    rq = orc.rope(orc.rms_norm(q, wq, eps, bf16, plus_one=plus_one), pos, cos, sin, rot, bf16)
+    rk = orc.rope(orc.rms_norm(k, wk, eps, bf16, plus_one=plus_one), pos, cos, sin, rot, bf16)
+    gq, gk = to_np(qo), to_np(ko)
+    for name, got, want in (("q", gq, rq), ("k", gk, rk)):
+        bad = ~((np.isnan(got) & np.isnan(want)) | (got.view(np.uint32) == want.view(np.uint32)))
+        if bad.any():
+            idx = np.argwhere(bad)[:5]
+            _say(f"{name} mismatches at {idx.tolist()}: got {got[tuple(idx.T)]}, want {want[tuple(idx.T)]}")
+        assert _same_bits(got, want), name

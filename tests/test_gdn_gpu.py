@@ -123,3 +123,33 @@ def test_gdn_c5_split_sequence(gpu):
     assert np.isfinite(full).all() and np.isfinite(to_np(so)).all()
     assert es <= F32_TOL
     assert ey <= BF16_TOL
+
+
+def test_gdn_graph_replay_matches_eager(gpu):
+    """The four GDN kernels captured once in a HIP graph give the eager
+    result on every replay (eager work and synchronisations in between)."""
+    import torch
+    w = configs.GdnWorkload("gdn-graph", 13, True, 2, 150, nk=2, nv=4)
+    inp = w.inputs()
+    dev = lambda x: to_dev(np.ascontiguousarray(x), True, gpu)
+    f32 = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu)
+    layer = cev_hip.GatedDeltaNet(w.batch, w.t, w.nk, w.nv, w.dk, w.dv, w.kernel, w.eps, dtype=torch.bfloat16, device=gpu)
+    xs = [dev(inp[k]) for k in ("mixed", "z", "b", "a", "conv_w")] + [f32(inp[k]) for k in ("neg_a", "dt_bias", "norm_w")]
+    y = torch.empty((w.batch, w.t, w.nv * w.dv), dtype=torch.bfloat16, device=gpu)
+    co = torch.empty((w.batch, layer.conv_dim, w.kernel - 1), dtype=torch.bfloat16, device=gpu)
+    so = torch.empty((w.batch, w.nv, w.dk, w.dv), dtype=torch.float32, device=gpu)
+    layer(*xs, y=y, conv_out=co, s_out=so)
+    torch.cuda.synchronize()
+    want = [to_np(t).copy() for t in (y, co, so)]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer(*xs, y=y, conv_out=co, s_out=so)
+    for i in range(3):
+        for t in (y, co, so):
+            t.fill_(float("nan"))
+        layer.workspace.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for got, ref in zip((y, co, so), want):
+            assert np.array_equal(to_np(got), ref), f"replay {i}"
