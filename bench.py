@@ -263,14 +263,118 @@ def bench_gdn(args, w, dev):
     print(json.dumps(res), flush=True)
 
 
+def cpu_baseline_stack(w, target_layers: int = 1):
+    """The oracle's restatement of one decoder layer of the packed pass
+    (f32 BLAS GEMMs with the model dtype's rounding points, the pinned
+    QK-norm + RoPE and candle-op attention with the engine mask, SwiGLU),
+    scaled by the layer count."""
+    import numpy as np
+
+    import oracle
+    from cev_hip import configs
+    from oracle.qwen3_stack import Qwen3Oracle
+    if not os.path.exists(oracle.LIB_PATH):
+        oracle.build()
+    w1 = configs.Qwen3StackWorkload(w.name, w.seed, w.bf16, n_layers=target_layers, vocab=4096)
+    o = Qwen3Oracle(w1, w1.weights())
+    state, qs, _ = w1.ids()
+    o.prefill(state[: w1.head_tokens], w1.prefill_chunk)
+    plans, items = w1.plans_items()
+    tokens = np.concatenate([state[w1.head_tokens:], qs.reshape(-1)])
+    ep = oracle.engine_pass(plans, items)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        o._layers(tokens, ep["pos"], ep["mask"])
+        times.append(time.perf_counter() - t0)
+    per_layer = statistics.median(times) / target_layers
+    return {
+        "value": w1.pass_tokens / (per_layer * w.n_layers),
+        "unit": "query tok/s",
+        "cores": oracle.threads(),
+        "kind": "port",
+        "sample": (f"{target_layers} decoder layer(s) of the packed pass ({w1.pass_tokens} tokens over a {w1.head_tokens}-token "
+                   f"cached head) through the oracle's restatement, scaled to {w.n_layers} layers; median of 3; CPU: {cpu_model()}"),
+    }
+
+
+def bench_stack(args, w, dev):
+    """Config 2: one step = one packed pass (the 512-token tail plus 64
+    question blocks of 48 tokens) through all 28 layers over the prefilled
+    1536-token head; the prefill is timed once beside it."""
+    import numpy as np
+    import torch
+
+    from cev_hip import BlockTable, device_info
+    from cev_hip.qwen3 import Qwen3Stack
+    dtype = torch.bfloat16 if w.bf16 else torch.float32
+    stack = Qwen3Stack(w, w.device_weights(dev, dtype), dev, capacity=w.state_tokens + w.questions * w.q_len)
+    torch.cuda.empty_cache()
+    state, qs, codes = w.ids()
+    stack.prefill(state[: w.head_tokens], w.prefill_chunk)  # warm-up (library GEMM selection)
+    stack.cached = 0
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    stack.prefill(state[: w.head_tokens], w.prefill_chunk)
+    e1.record()
+    torch.cuda.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+    plans, items = w.plans_items()
+    table, pos, gather = BlockTable.from_plans(plans, items)
+    tokens = np.concatenate([state[w.head_tokens:], qs.reshape(-1)])
+
+    def step():
+        return stack.code_logits(stack.forward_packed(tokens, pos, table, gather), codes)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record()
+        step()
+        b.record()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    pass_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    fl = w.flops()
+    dt = "bf16" if w.bf16 else "f32"
+    res = {
+        "metric": METRIC,
+        "value": w.pass_tokens / (ms_step * 1e-3),
+        "unit": "query tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": dt,
+        "data": "synthetic (random token ids; weights N(0, 0.02) drawn on the device, norm weights 1)",
+        "config": {"workload": f"c2: Qwen3-1.7B-shaped stack ({w.n_layers} layers, hidden {w.hidden}, Hq={w.hq}, Hkv={w.hkv}, "
+                               f"d={w.d}, intermediate {w.inter}, vocab {w.vocab}), one packed pass of {w.pass_tokens} tokens "
+                               f"(tail {w.state_tokens - w.head_tokens} + {w.questions} x {w.q_len}) over a {w.head_tokens}-token "
+                               f"prefilled head, code-head logits over {w.n_codes} codes",
+                   "launch": "direct launches"},
+        "tflops": fl["pass"] / (ms_step * 1e-3) / 1e12,
+        "pass_ms": pass_ms,
+        "prefill_ms": prefill_ms,
+        "prefill_tflops": fl["prefill"] / (prefill_ms * 1e-3) / 1e12,
+        "roofline": roofline(fl["pass"], 1, pass_ms, dt, "whole pass (library GEMMs + K1 + K2 + norms + SwiGLU)", None),
+        "device": device_info().name,
+    }
+    res["roofline"]["alg_bytes"] = None
+    if args.cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_stack(w)
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "c4", "c5a", "hbm", "c5gdn", "c5gdnrows"],
-                    help="c3 (default): the 32k-prefix packed-prefill attention; c5gdn / c5gdnrows: the Gated DeltaNet "
-                         "layer core over one 4096-token row / 32 rows of 64 tokens")
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5a", "hbm", "c5gdn", "c5gdnrows"],
+                    help="c3 (default): the 32k-prefix packed-prefill attention; c2: the Qwen3-1.7B-shaped stack's packed "
+                         "pass; c5gdn / c5gdnrows: the Gated DeltaNet layer core over one 4096-token row / 32 rows of 64 tokens")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline leg")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: capture each timed call once in a HIP graph and replay it; 0 (default): launch directly (graph launch costs more than it saves here)")
@@ -297,6 +401,9 @@ def main():
         return
     if args.workload == "c5gdn":
         bench_gdn(args, configs.c5_gdn(), dev)
+        return
+    if args.workload == "c2":
+        bench_stack(args, configs.c2(True), dev)
         return
     if args.workload == "c5gdnrows":
         bench_gdn(args, configs.GdnWorkload("c5gdn32x64", 5, True, 32, 64), dev)

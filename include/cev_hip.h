@@ -226,6 +226,28 @@ int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, const void* z,
                         void* conv_out, float* s_out, void* workspace, size_t workspace_bytes, cev_stream stream);
 
 /* ------------------------------------------------------------------ */
+/* Decoder-layer pieces around attention (Qwen3 stack, config-2 passes). */
+
+/* RMSNorm of `rows` rows of `hidden` elements, candle_nn RmsNorm in the
+ * model dtype (input_layernorm / post_attention_layernorm / final norm,
+ * crates/cev-model/src/qwen3.rs:254-255, :400): y = dtype(dtype(x / m) * w),
+ * m = dtype(sqrt(sum x^2 / hidden + eps)), the sum in element order.
+ * With h != NULL the residual add before the norm is fused in
+ * (qwen3.rs:261 in mlp_block, :358 and :397): x_out = dtype(x + h) is written
+ * (x_out may alias x) and normalised.  weight_plus_one selects 1 + w.
+ * Strides are in elements; rows and buffers 16-byte aligned. */
+int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h, int64_t h_stride,
+                     void* x_out, int64_t x_out_stride, const void* w, float eps, int32_t weight_plus_one, void* y, int64_t y_stride,
+                     cev_stream stream);
+
+/* The SwiGLU of Mlp::forward (qwen3.rs:230-233): out = dtype(silu(gate) * up),
+ * silu(v) = v / (1 + exp(-v)) with each op in the model dtype.  gate and up
+ * share the row stride in_stride (e.g. the two halves of one fused GEMM
+ * output). */
+int32_t cev_swiglu(int32_t dtype, int64_t rows, int32_t inter, const void* gate, const void* up, int64_t in_stride, void* out,
+                   int64_t out_stride, cev_stream stream);
+
+/* ------------------------------------------------------------------ */
 /* Table builders (host only). */
 
 /* The packed pass of engine.rs:365-442.  Plans p = 0..n_plans-1 in plan

@@ -318,6 +318,40 @@ def qknorm_rope(q_in, k_in, w_q, w_k, pos, rot: Rotary, eps: float, plus_one: bo
     return q_out, k_out
 
 
+def rms_norm(x, w, eps: float, h=None, x_out=None, y=None, plus_one: bool = False, stream=None):
+    """candle_nn RmsNorm over the last dim of a (rows, hidden) view in the
+    model dtype (qwen3.rs:254-255, :400); with h, the residual add before it
+    (qwen3.rs:261, :358, :397): x_out = x + h is written (x_out may be x)
+    and normalised.  Returns y."""
+    torch = _torch()
+    rows, hidden = x.shape
+    if y is None:
+        y = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
+    if h is not None and x_out is None:
+        x_out = x
+    for t_ in (x, y, w) + ((h, x_out) if h is not None else ()):
+        if t_.stride(-1) != 1 or t_.dtype != x.dtype:
+            raise CevError(-2, "rms_norm: tensors must share the dtype and have a contiguous last dim")
+    check(lib().cev_rms_norm(_dtype_code(x), rows, hidden, _ptr(x), x.stride(0), _ptr(h), h.stride(0) if h is not None else 0,
+                             _ptr(x_out), x_out.stride(0) if x_out is not None else 0, _ptr(w), float(eps), 1 if plus_one else 0,
+                             _ptr(y), y.stride(0), _stream_ptr(stream)))
+    return y
+
+
+def swiglu(gate, up, out=None, stream=None):
+    """silu(gate) * up in the model dtype (Mlp::forward, qwen3.rs:230-233);
+    gate and up are (rows, inter) views sharing a row stride."""
+    torch = _torch()
+    rows, inter = gate.shape
+    if up.shape != gate.shape or up.stride(0) != gate.stride(0):
+        raise CevError(-1, "swiglu: gate and up must have the same shape and row stride")
+    if out is None:
+        out = torch.empty((rows, inter), dtype=gate.dtype, device=gate.device)
+    check(lib().cev_swiglu(_dtype_code(gate), rows, inter, _ptr(gate), _ptr(up), gate.stride(0), _ptr(out), out.stride(0),
+                           _stream_ptr(stream)))
+    return out
+
+
 @dataclass
 class DeviceInfo:
     name: str

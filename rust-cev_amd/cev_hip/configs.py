@@ -202,3 +202,137 @@ class GdnWorkload:
 
 def c5_gdn(t: int = 4096, batch: int = 1) -> GdnWorkload:
     return GdnWorkload(f"c5gdn{batch}x{t}", 5, True, batch, t)
+
+
+@dataclass
+class Qwen3StackWorkload:
+    """Config 2: a Qwen3-1.7B-shaped decoder stack (28 layers, hidden 2048,
+    Hq = 16, Hkv = 8, d = 128, intermediate 6144, vocab 151936, tied
+    embeddings, eps 1e-6, theta 1e6) with random weights N(0, 0.02) and norm
+    weights 1.  A 2048-token state of uniform token ids: its first 1536
+    tokens are prefilled in 512-token chunks (qwen3.rs:346-362), the last 512
+    (the tail) ride along in one packed pass with 64 question blocks of 48
+    tokens (engine.rs:236-287, :365-442); the readout is the final-normed
+    hidden state at the 64 gather positions times 8 code rows of the tied
+    head (engine.rs:155, :463-469).
+
+    Weights come from numpy's PCG64, one seeded stream per tensor (the
+    splitmix64 streams of the attention configs are too slow for 1.7e9
+    values); token ids from PCG64 too."""
+    name: str
+    seed: int
+    bf16: bool
+    n_layers: int = 28
+    hidden: int = 2048
+    hq: int = 16
+    hkv: int = 8
+    d: int = 128
+    inter: int = 6144
+    vocab: int = 151936
+    eps: float = 1e-6
+    theta: float = 1e6
+    state_tokens: int = 2048
+    prefill_chunk: int = 512
+    questions: int = 64
+    q_len: int = 48
+    n_codes: int = 8
+    std: float = 0.02
+
+    @property
+    def head_tokens(self) -> int:
+        """Tokens prefilled before the pass: all but the last chunk (engine.rs:251-253)."""
+        return self.state_tokens - min(self.state_tokens, self.prefill_chunk)
+
+    @property
+    def pass_tokens(self) -> int:
+        return self.state_tokens - self.head_tokens + self.questions * self.q_len
+
+    def _normal(self, stream: int, shape):
+        g = np.random.Generator(np.random.PCG64(np.random.SeedSequence([self.seed, stream])))
+        x = g.standard_normal(int(np.prod(shape)), dtype=np.float32).reshape(shape)
+        x *= np.float32(self.std)
+        return x
+
+    def weights(self, threads: int = 8) -> dict:
+        """{name: f32 array} in the layout of torch / candle Linear (out, in);
+        bf16 configs hold bf16-representable values."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        from .synth import round_bf16
+        specs = self.weight_specs()
+
+        def make(spec):
+            name, stream, shape = spec
+            x = self._normal(stream, shape)
+            return name, round_bf16(x) if self.bf16 else x
+
+        with ThreadPoolExecutor(threads) as ex:
+            w = dict(ex.map(make, specs))
+        w.update({name: np.ones(n, np.float32) for name, n in self.norm_specs()})
+        return w
+
+    def weight_specs(self):
+        """(name, PCG64 stream, shape) of every random matrix."""
+        H, d = self.hidden, self.d
+        specs = [("embed", 1, (self.vocab, H))]
+        for i in range(self.n_layers):
+            base = 100 + 16 * i
+            specs += [(f"l{i}.wq", base, (self.hq * d, H)), (f"l{i}.wk", base + 1, (self.hkv * d, H)),
+                      (f"l{i}.wv", base + 2, (self.hkv * d, H)), (f"l{i}.wo", base + 3, (H, self.hq * d)),
+                      (f"l{i}.gate", base + 4, (self.inter, H)), (f"l{i}.up", base + 5, (self.inter, H)),
+                      (f"l{i}.down", base + 6, (H, self.inter))]
+        return specs
+
+    def norm_specs(self):
+        """(name, length) of every norm weight (all ones)."""
+        out = []
+        for i in range(self.n_layers):
+            out += [(f"l{i}.q_norm", self.d), (f"l{i}.k_norm", self.d), (f"l{i}.ln1", self.hidden), (f"l{i}.ln2", self.hidden)]
+        return out + [("norm", self.hidden)]
+
+    def device_weights(self, device, dtype):
+        """Random weights of the same shapes drawn on the device (torch's
+        generator, not the PCG64 streams): for timing runs, where the values
+        only need the right distribution."""
+        import torch
+        g = torch.Generator(device=device).manual_seed(self.seed)
+        w = {}
+        for name, _, shape in self.weight_specs():
+            w[name] = (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * self.std).to(dtype)
+        for name, n in self.norm_specs():
+            w[name] = torch.ones(n, device=device, dtype=dtype)
+        return w
+
+    def ids(self):
+        """(state ids, question ids (questions, q_len), code ids)."""
+        g = np.random.Generator(np.random.PCG64(np.random.SeedSequence([self.seed, 2])))
+        state = g.integers(0, self.vocab, self.state_tokens, dtype=np.int64)
+        qs = g.integers(0, self.vocab, (self.questions, self.q_len), dtype=np.int64)
+        codes = g.choice(self.vocab, self.n_codes, replace=False).astype(np.int64)
+        return state, qs, codes
+
+    def plans_items(self):
+        """One plan (past = head, prefix = state, tail = the rest) and its questions."""
+        return [(self.head_tokens, self.state_tokens, self.head_tokens)], [(0, self.q_len)] * self.questions
+
+    def flops(self) -> dict:
+        """Useful FLOPs of the prefill and of the pass: linear layers (2 per
+        multiply-add) and attention (unmasked pairs x 4d)."""
+        H, I, d, L = self.hidden, self.inter, self.d, self.n_layers
+        lin = 2 * (H * (self.hq + 2 * self.hkv) * d + self.hq * d * H + 3 * H * I)
+        out = {}
+        past, pre = 0, 0
+        for n in [self.prefill_chunk] * (self.head_tokens // self.prefill_chunk) + (
+                [self.head_tokens % self.prefill_chunk] if self.head_tokens % self.prefill_chunk else []):
+            pre += lin * n + 4 * d * self.hq * (n * past + n * (n + 1) // 2)
+            past += n
+        out["prefill"] = float(pre * L)
+        tail = self.state_tokens - self.head_tokens
+        pairs = tail * self.head_tokens + tail * (tail + 1) // 2
+        pairs += self.questions * (self.q_len * self.state_tokens + self.q_len * (self.q_len + 1) // 2)
+        out["pass"] = float(L * (lin * self.pass_tokens + 4 * d * self.hq * pairs))
+        return out
+
+
+def c2(bf16: bool = True, **kw) -> Qwen3StackWorkload:
+    return Qwen3StackWorkload("c2" if bf16 else "c2-f32", 2, bf16, **kw)

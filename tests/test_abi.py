@@ -131,6 +131,34 @@ def test_qknorm_validation(cev):
     assert L.cev_qknorm_rope(C.byref(d), None, None, None, None, None, None, None, None, None, None) == CEV_ERR_UNSUPPORTED
 
 
+def test_layer_norm_and_swiglu_validation(cev):
+    """cev_rms_norm / cev_swiglu refuse bad shapes, null and misaligned
+    buffers and short strides before any launch (no GPU needed)."""
+    L = _abi.lib()
+    buf = (C.c_uint8 * 4096)()
+    a = C.addressof(buf)
+    al = a + (-a) % 16
+    p = C.c_void_p(al)
+    odd = C.c_void_p(al + 2)
+    # dtype, hidden not a multiple of 8 (bf16) / 4 (f32), negative eps
+    assert L.cev_rms_norm(7, 4, 64, p, 64, None, 0, None, 0, p, 1e-6, 0, p, 64, None) == CEV_ERR_UNSUPPORTED
+    assert L.cev_rms_norm(CEV_BF16, 4, 60, p, 64, None, 0, None, 0, p, 1e-6, 0, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_rms_norm(CEV_F32, 4, 62, p, 64, None, 0, None, 0, p, 1e-6, 0, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_rms_norm(CEV_BF16, 4, 64, p, 64, None, 0, None, 0, p, -1.0, 0, p, 64, None) == CEV_ERR_INVALID
+    # null, misaligned, strides shorter than a row or breaking 16-byte rows
+    assert L.cev_rms_norm(CEV_BF16, 4, 64, None, 64, None, 0, None, 0, p, 1e-6, 0, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_rms_norm(CEV_BF16, 4, 64, p, 64, p, 64, None, 0, p, 1e-6, 0, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_rms_norm(CEV_BF16, 4, 64, odd, 64, None, 0, None, 0, p, 1e-6, 0, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_rms_norm(CEV_BF16, 4, 64, p, 32, None, 0, None, 0, p, 1e-6, 0, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_rms_norm(CEV_BF16, 4, 64, p, 68, None, 0, None, 0, p, 1e-6, 0, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_rms_norm(CEV_BF16, 0, 64, None, 0, None, 0, None, 0, None, 1e-6, 0, None, 0, None) == 0  # nothing to do
+    assert L.cev_swiglu(CEV_BF16, 4, 60, p, p, 64, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_swiglu(CEV_BF16, 4, 64, p, None, 64, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_swiglu(CEV_BF16, 4, 64, p, odd, 64, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_swiglu(CEV_BF16, 4, 64, p, p, 40, p, 64, None) == CEV_ERR_INVALID
+    assert L.cev_swiglu(CEV_BF16, 0, 64, None, None, 0, None, 0, None) == 0
+
+
 # ---------------------------------------------------------------- table builders vs reference masks
 
 
