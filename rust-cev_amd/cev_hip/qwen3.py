@@ -24,7 +24,7 @@ from . import BlockTable, PackedAttention, Rotary, qknorm_rope, rms_norm, swiglu
 
 
 class Qwen3Stack:
-    def __init__(self, w, weights: dict, device, capacity: int, dtype=None):
+    def __init__(self, w, weights: dict, device, capacity: int, dtype=None, max_splits: int = 0):
         """w: a Qwen3StackWorkload (shapes); weights: {name: array} as made
         by w.weights() (numpy) or w.device_weights() (torch); capacity: K/V
         cache slots per layer."""
@@ -56,6 +56,7 @@ class Qwen3Stack:
         self.capacity = capacity
         self.rot = Rotary(w.theta, w.d, capacity, self.dtype, device)
         self.cached = 0  # tokens in the K/V caches
+        self.max_splits = max_splits  # split policy of the attention plans (0: the planner's)
 
     def _run(self, tokens, pos, table: BlockTable, keep: bool) -> "torch.Tensor":
         """All layers over the packed new tokens; their K/V land in cache
@@ -92,7 +93,7 @@ class Qwen3Stack:
             kc, vc = L["k"][:, :s0], L["v"][:, :s0]
             if attn is None:
                 attn = PackedAttention(q, k_new, table, k_cache=kc if s0 else None, s_cache=s0, out=o, v_new=v_new,
-                                       v_cache=vc if s0 else None)
+                                       v_cache=vc if s0 else None, max_splits=self.max_splits)
             attn(q, k_new, v_new, kc if s0 else None, vc if s0 else None, None, o)
             h = torch.matmul(o.view(t, hq * d), L["wo"].t())
             rms_norm(x, L["ln2"], w.eps, h=h, x_out=x, y=y)  # x += h; y = ln2(x)

@@ -326,19 +326,30 @@ int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, P
     }
     oi = oj;
   }
-  // Split the key stream of every tile when the tiles alone leave the GPU
-  // underfilled (few long-prefix rows): each part still gets at least
-  // kSplitMinChunks key tiles.
+  // Split the key stream of every tile when that shortens the launch (few
+  // long-prefix rows leave the GPU underfilled): each part still gets at
+  // least kSplitMinChunks key tiles.
   int32_t max_chunks = 0;
   for (int32_t ti = 0; ti < p.n_tiles; ++ti) max_chunks = std::max(max_chunks, p.tiles[(size_t)ti * 8 + 4]);
   const int64_t items = (int64_t)p.n_tiles * d->n_kv_heads;
   int64_t split = 1;
   if (items > 0 && d->max_splits != 1) {
-    split = (kSplitTargetWorkgroups + items - 1) / items;
-    split = std::min<int64_t>(split, std::max(1, max_chunks / kSplitMinChunks));
-    split = std::min<int64_t>(split, kSplitMax);
-    if (d->max_splits > 1) split = std::min<int64_t>(split, d->max_splits);
-    split = std::max<int64_t>(split, 1);
+    // Unsplit, or split into parts that fit one round of
+    // kSplitTargetWorkgroups workgroups, whichever has the smaller modelled
+    // time: rounds x the longest part's chunks, plus the merge pass when
+    // split; on a tie the larger part count (a fuller round).
+    int64_t cap = std::min<int64_t>(std::max(1, max_chunks / kSplitMinChunks), kSplitMax);
+    if (d->max_splits > 1) cap = std::min<int64_t>(cap, d->max_splits);
+    cap = std::min<int64_t>(cap, std::max<int64_t>(1, kSplitTargetWorkgroups / items));
+    int64_t best = -1;
+    for (int64_t sp = 1; sp <= cap; ++sp) {
+      const int64_t rounds = (items * sp + kSplitTargetWorkgroups - 1) / kSplitTargetWorkgroups;
+      const int64_t cost = rounds * ((max_chunks + sp - 1) / sp) + (sp > 1 ? kSplitMergeChunks : 0);
+      if (best < 0 || cost <= best) {
+        best = cost;
+        split = sp;
+      }
+    }
   }
   p.n_splits = (int32_t)split;
   return CEV_OK;

@@ -51,11 +51,16 @@ CEV_HD static inline int cev_attn_block_n(int dtype, int head_dim) { return (dty
 // units) and the sum l, padded to keep records 16-byte aligned.
 CEV_HD static inline int64_t cev_attn_partial_floats(int head_dim) { return (int64_t)head_dim + 4; }
 
-// Split policy: aim for one round of workgroups on MI355X (256 CUs, one
-// attention workgroup per CU: its LDS and 8 waves of >128 VGPRs fill a
-// CU), never cut a tile's key stream into parts of fewer than
-// kSplitMinChunks key tiles.  Measured on the 32k-prefix x 16-token shape:
-// 32 parts per KV head (256 workgroups) 38 us, 64 parts 49 us.
+// Split policy.  One attention workgroup fills a CU (its LDS and 8 waves of
+// >128 VGPRs), so a launch runs in rounds of 256 workgroups on MI355X.  The
+// planner keeps the tiles whole or splits them into parts that fit one
+// round, whichever minimises rounds x chunks of the longest part + the
+// merge pass (counted as kSplitMergeChunks chunk steps), never cutting a key
+// stream into parts of fewer than kSplitMinChunks chunks.  Measured: the
+// 32k-prefix x 16-token shape (8 tile x head items) 32 parts 38 us, 64
+// parts 49 us; the config-2 pass (224 items) unsplit 14.0 ms, 2 parts
+// 14.9 ms.
 constexpr int kSplitTargetWorkgroups = 256;
 constexpr int kSplitMinChunks = 4;
+constexpr int kSplitMergeChunks = 3;
 constexpr int kSplitMax = 256;

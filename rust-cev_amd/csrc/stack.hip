@@ -11,17 +11,32 @@
 //                 op in the model dtype (Mlp::forward, qwen3.rs:230-233).
 // The projections around them are plain GEMMs (the library's).
 //
-// Norm work split: a workgroup takes kNormRows rows.  Lanes 0..kNormRows-1
-// of wave 0 each sum one row's squares in element order (the reference's
-// sequential f32 sum, bit for bit); then all 256 threads normalise the rows
-// with coalesced 16-byte accesses.
+// Norm work split: a workgroup takes up to kNormRows rows.  All 1024 threads
+// load them with coalesced 16-byte accesses (x + h for the fused residual,
+// written back as they go), keep their chunks in registers and put the
+// squares, as f32, in LDS; lanes 0..rows-1 of wave 0 then each add one row's
+// squares in element order (the reference's sequential f32 sum, bit for bit:
+// one dependent add per element), and every thread normalises its own
+// chunks.  Rows of squares sit 16 bytes apart beyond their length, so the
+// summing lanes' 16-byte reads fall on different banks.
+//
+// x / m is correctly rounded for every element.  With y = RN(1/m),
+// q0 = RN(x y) and the exact residual r = x - q0 m, RN(q0 + r y) is the
+// correctly rounded quotient (Markstein) while r can neither underflow nor
+// overflow: every nonzero |x| in [2^-96, 2^60] (the sum of squares <= 2^120
+// bounds the top) and m in [2^-20, 2^20].  A row outside that range takes
+// the IEEE division; copysign keeps the sign of -0 / m.
+#include <algorithm>
+
 #include "cev_device.h"
 #include "cev_internal.h"
 
 namespace {
 
-constexpr int kNormThreads = 256;
-constexpr int kNormRows = 16;
+constexpr int kNormThreads = 1024;
+constexpr int kNormRows = 16;                   // rows per workgroup at most
+constexpr int kNormLdsBytes = 132 * 1024;       // LDS for the rows' squares
+constexpr int kNormChunks = 4;                  // 16-byte chunks each thread keeps in registers
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -63,60 +78,108 @@ __device__ __forceinline__ u32x4 pack(const float* v) {
   return c;
 }
 
+// LDS pitch in bytes of one row of f32 squares.
+__host__ __device__ inline int norm_pitch(int hidden) { return hidden * 4 + 16; }
+
 template <typename T>
-__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a, int rows_per_wg) {
   constexpr bool BF = sizeof(T) == 2;
   constexpr int VEC = 16 / (int)sizeof(T);
   auto rnd = [](float v) { return BF ? bf16_round(v) : v; };
-  __shared__ float msh[kNormRows];
-  const int64_t r0 = (int64_t)blockIdx.x * kNormRows;
-  const int nrows = (int)min<int64_t>(kNormRows, a.rows - r0);
+  extern __shared__ __align__(16) char sq_lds[];
+  __shared__ float msh[kNormRows], ysh[kNormRows];
+  __shared__ int min_exp[kNormRows], fast_row[kNormRows];
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_wg;
+  const int nrows = (int)min<int64_t>(rows_per_wg, a.rows - r0);
   const int nc = a.hidden / VEC;
+  const int pitch = norm_pitch(a.hidden);
   const int tid = threadIdx.x;
+  const int total = nrows * nc;  // <= kNormThreads * kNormChunks (launcher)
+  if (tid < kNormRows) min_exp[tid] = 0;
+  __syncthreads();
 
-  if (tid < nrows) {
-    const int64_t r = r0 + tid;
-    const T* xr = (const T*)a.x + r * a.x_st;
-    const T* hr = a.h ? (const T*)a.h + r * a.h_st : nullptr;
-    float s = 0.0f;
-#pragma unroll 4
-    for (int k = 0; k < nc; ++k) {
-      const u32x4 cx = *(const u32x4*)(xr + k * VEC);
-      u32x4 ch = {};
-      if (hr) ch = *(const u32x4*)(hr + k * VEC);
+  // chunk b of this thread is i = tid + b * kNormThreads
+  u32x4 cx[kNormChunks];
+  {
+    u32x4 ch[kNormChunks];
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const float v = hr ? rnd(elem<T>(cx, j) + elem<T>(ch, j)) : elem<T>(cx, j);
-        s += v * v;
+    for (int b = 0; b < kNormChunks; ++b) {
+      const int i = tid + b * kNormThreads;
+      if (i < total) {
+        const int64_t r = r0 + i / nc;
+        const int k = i % nc;
+        cx[b] = *(const u32x4*)((const T*)a.x + r * a.x_st + k * VEC);
+        if (a.h) ch[b] = *(const u32x4*)((const T*)a.h + r * a.h_st + k * VEC);
       }
     }
-    msh[tid] = rnd(sqrtf(s / (float)a.hidden + a.eps));
+#pragma unroll
+    for (int b = 0; b < kNormChunks; ++b) {
+      const int i = tid + b * kNormThreads;
+      if (i < total) {
+        const int rr = i / nc, k = i % nc;
+        float xs[VEC];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) xs[j] = a.h ? rnd(elem<T>(cx[b], j) + elem<T>(ch[b], j)) : elem<T>(cx[b], j);
+        if (a.h) {
+          cx[b] = pack<T>(xs);
+          *(u32x4*)((T*)a.x_out + (r0 + rr) * a.xo_st + k * VEC) = cx[b];
+        }
+        int me = 0;
+        float* sq = (float*)(sq_lds + rr * pitch) + k * VEC;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          sq[j] = xs[j] * xs[j];
+          me = min(me, __builtin_amdgcn_frexp_expf(xs[j]));
+        }
+        if (me < 0) atomicMin(&min_exp[rr], me);
+      }
+    }
   }
   __syncthreads();
 
-  for (int i = tid; i < nrows * nc; i += kNormThreads) {
-    const int rr = i / nc, k = i % nc;
-    const int64_t r = r0 + rr;
-    const float m = msh[rr];
-    const u32x4 cx = *(const u32x4*)((const T*)a.x + r * a.x_st + k * VEC);
-    const u32x4 cw = *(const u32x4*)((const T*)a.w + k * VEC);
-    float xs[VEC], ys[VEC];
-    if (a.h) {
-      const u32x4 ch = *(const u32x4*)((const T*)a.h + r * a.h_st + k * VEC);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) xs[j] = rnd(elem<T>(cx, j) + elem<T>(ch, j));
-      *(u32x4*)((T*)a.x_out + r * a.xo_st + k * VEC) = pack<T>(xs);
-    } else {
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) xs[j] = elem<T>(cx, j);
+  if (tid < nrows) {
+    const float* row = (const float*)(sq_lds + tid * pitch);
+    float s = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < a.hidden / 4; ++k) {
+      const f32x4 q = *(const f32x4*)(row + 4 * k);
+      s += q[0];
+      s += q[1];
+      s += q[2];
+      s += q[3];
     }
+    const float m = rnd(sqrtf(s / (float)a.hidden + a.eps));
+    msh[tid] = m;
+    ysh[tid] = 1.0f / m;
+    fast_row[tid] = min_exp[tid] >= -95 && s <= 0x1p120f && m >= 0x1p-20f && m <= 0x1p20f;
+  }
+  __syncthreads();
+
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      float w = elem<T>(cw, j);
-      if (a.plus_one) w = rnd(w + 1.0f);
-      ys[j] = rnd(rnd(xs[j] / m) * w);
+  for (int b = 0; b < kNormChunks; ++b) {
+    const int i = tid + b * kNormThreads;
+    if (i < total) {
+      const int rr = i / nc, k = i % nc;
+      const float m = msh[rr], y = ysh[rr];
+      const bool fast = fast_row[rr];
+      const u32x4 cw = *(const u32x4*)((const T*)a.w + k * VEC);
+      float ys[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float x = elem<T>(cx[b], j);
+        float q;
+        if (fast) {
+          const float q0 = x * y;
+          q = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, m, x), y, q0), q0);
+        } else {
+          q = x / m;
+        }
+        float w = elem<T>(cw, j);
+        if (a.plus_one) w = rnd(w + 1.0f);
+        ys[j] = rnd(rnd(q) * w);
+      }
+      *(u32x4*)((T*)a.y + (r0 + rr) * a.y_st + k * VEC) = pack<T>(ys);
     }
-    *(u32x4*)((T*)a.y + r * a.y_st + k * VEC) = pack<T>(ys);
   }
 }
 
@@ -176,13 +239,17 @@ extern "C" int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, con
                     (!h || (h_stride >= hidden && x_out_stride >= hidden && h_stride % vec == 0 && x_out_stride % vec == 0)),
                 "cev_rms_norm: row strides must cover a row and keep rows 16-byte aligned");
   NormArgs a{x, h, x_out, w, y, rows, x_stride, h_stride, x_out_stride, y_stride, hidden, weight_plus_one, eps};
-  const int64_t grid = (rows + kNormRows - 1) / kNormRows;
+  const int pitch = norm_pitch(hidden);
+  const int rows_per_wg = std::min({kNormRows, kNormLdsBytes / pitch, kNormThreads * kNormChunks / (hidden / vec)});
+  CEV_CHECK_ARG(rows_per_wg >= 1, "cev_rms_norm: hidden %d too large for one row in LDS", hidden);
+  const int64_t grid = (rows + rows_per_wg - 1) / rows_per_wg;
   if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "cev_rms_norm: too many rows");
   hipStream_t s = (hipStream_t)stream;
+  const size_t lds = (size_t)rows_per_wg * pitch;
   if (dtype == CEV_BF16)
-    hipLaunchKernelGGL(rms_norm_kernel<uint16_t>, dim3((unsigned)grid), dim3(kNormThreads), 0, s, a);
+    hipLaunchKernelGGL(rms_norm_kernel<uint16_t>, dim3((unsigned)grid), dim3(kNormThreads), lds, s, a, rows_per_wg);
   else
-    hipLaunchKernelGGL(rms_norm_kernel<float>, dim3((unsigned)grid), dim3(kNormThreads), 0, s, a);
+    hipLaunchKernelGGL(rms_norm_kernel<float>, dim3((unsigned)grid), dim3(kNormThreads), lds, s, a, rows_per_wg);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "cev_rms_norm launch: %s", hipGetErrorString(e));
   return CEV_OK;

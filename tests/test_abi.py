@@ -278,6 +278,19 @@ def test_split_policy(cev):
     tab, _, _ = cev_hip.BlockTable.from_plans(plans, items)
     d = cev_hip.attn_desc(CEV_BF16, 32, 8, 128, tab.t, tab.s_cache)
     assert cev_hip.AttnPlan(d, tab).n_splits == 1
+    # one round of 256 workgroups: the 16-token shape takes 32 parts (8 x 32)
+    d = cev_hip.attn_desc(CEV_BF16, 32, 8, 128, 16, 32768)
+    assert cev_hip.AttnPlan(d, hbm).n_splits == 32
+    # 224 workgroups already fill the round: splitting would add a second
+    # round and the merge (the config-2 pass)
+    tab, _, _ = cev_hip.BlockTable.from_plans([(1536, 2048, 1536)], [(0, 48)] * 64)
+    d = cev_hip.attn_desc(CEV_BF16, 16, 8, 128, tab.t, tab.s_cache)
+    p = cev_hip.AttnPlan(d, tab)
+    assert p.n_tiles * 8 == 224 and p.n_splits == 1
+    # 128 workgroups of long rows: two parts fill the round (the gated rows)
+    tab = cev_hip.BlockTable.from_rows(32, 64, 4096, causal=True)
+    d = cev_hip.attn_desc(CEV_BF16, 16, 4, 256, tab.t, tab.s_cache, has_gate=True)
+    assert cev_hip.AttnPlan(d, tab).n_splits == 2
 
 
 def test_launch_requires_workspace_for_split_plans(cev):

@@ -48,6 +48,47 @@ def _gpu_config(w, weights, device, second_pass=False):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("rows,hidden,residual", [(3584, 2048, False), (37, 2048, True), (5, 4096, True), (1, 64, False)])
+def test_layer_norm_bit_exact(gpu, orc, bf16, rows, hidden, residual):
+    """cev_rms_norm (with and without the fused residual add, row counts that
+    leave a partial workgroup) against the oracle's rms_norm bit for bit;
+    x_out aliases x as in the stack."""
+    import cev_hip
+    from helpers import to_dev
+    rng = np.random.default_rng(rows + hidden)
+    x = rng.standard_normal((rows, hidden)).astype(np.float32) * 3
+    h = rng.standard_normal((rows, hidden)).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    if bf16:
+        x, h, w = orc.round_bf16(x), orc.round_bf16(h), orc.round_bf16(w)
+    dx, dh, dw = to_dev(x, bf16, gpu), to_dev(h, bf16, gpu), to_dev(w, bf16, gpu)
+    y = cev_hip.rms_norm(dx, dw, 1e-6, h=dh if residual else None, x_out=dx if residual else None)
+    xs = (orc.round_bf16(x + h) if bf16 else (x + h)) if residual else x
+    want = orc.rms_norm(xs, w, 1e-6, bf16)
+    assert np.array_equal(to_np(y), want)
+    if residual:
+        assert np.array_equal(to_np(dx), xs)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_swiglu_matches_oracle(gpu, bf16):
+    import cev_hip
+    from helpers import to_dev
+    from oracle.qwen3_stack import _silu_mul
+    rng = np.random.default_rng(3)
+    gu = rng.standard_normal((300, 2 * 1024)).astype(np.float32) * 2
+    if bf16:
+        from oracle import round_bf16
+        gu = round_bf16(gu)
+    d = to_dev(gu, bf16, gpu)
+    out = to_np(cev_hip.swiglu(d[:, :1024], d[:, 1024:]))
+    want = _silu_mul(gu[:, :1024], gu[:, 1024:], bf16)
+    # exp may differ by an ulp between libm and the device; bf16 then by at most one bf16 step
+    tol = 2.0 ** -7 if bf16 else 2e-6
+    assert np.all(np.abs(out - want) <= tol * np.maximum(np.abs(want), 1e-3))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
 def test_stack_two_layers_vs_oracle(gpu, orc, bf16):
     """Config 2's widths and token layout at 2 layers and a 4096-token vocab."""
     from oracle.qwen3_stack import Qwen3Oracle, softmax64
