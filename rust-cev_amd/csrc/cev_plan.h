@@ -58,8 +58,8 @@ CEV_HD static inline int64_t cev_attn_partial_floats(int head_dim) { return (int
 // merge pass (counted as kSplitMergeChunks chunk steps), never cutting a key
 // stream into parts of fewer than kSplitMinChunks chunks.  Measured: the
 // 32k-prefix x 16-token shape (8 tile x head items) 32 parts 38 us, 64
-// parts 49 us; the config-2 pass (224 items) unsplit 14.0 ms, 2 parts
-// 14.9 ms.
+// parts 49 us; the config-2 pass's attention (224 items) unsplit 86.7 us,
+// 2 parts 119.8 us.
 constexpr int kSplitTargetWorkgroups = 256;
 constexpr int kSplitMinChunks = 4;
 constexpr int kSplitMergeChunks = 3;
