@@ -20,6 +20,8 @@
 // holds B[l/16][l%16], D lane l register r holds D[4(l/16)+r][l%16].
 #include <cstring>
 
+#include <type_traits>
+
 #include "cev_device.h"
 #include "cev_internal.h"
 
@@ -466,10 +468,21 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// scan: one workgroup (4 waves) per (row, value head, 16-column slice of the
+// scan: one workgroup (8 waves) per (row, value head, 16-column slice of the
 // state).  Per chunk (qwen35.rs:353-364):
 //   v_new = new_values - k_cumdecay . S;   out = (q e^cum) . S + intra . v_new;
 //   S = S e^last + (k e^(last-cum))^T . v_new.
+// Only v_new and the state update carry the recurrence; the output terms do
+// not, so they are spread to fill the second phase:
+//   phase A (all 8 waves): wave (row tile rt = w % 4, K half kh = w / 4)
+//     forms rows 16rt.. of k_cumdecay . S over its half of dk (16 MFMAs);
+//     kh = 0 writes new_values - that, kh = 1 writes its partial;
+//   phase B: every wave updates state rows 16w.. in place ((k e^(last-cum))^T
+//     . v_new, 16 MFMAs), forms its half of (q e^cum) . S from the state
+//     operands it read in phase A (16 MFMAs) and its blocks of intra . v_new
+//     (rows 16rt.., blocks kh and kh + 2 up to the diagonal); kh = 0 keeps
+//     its sum, kh = 1 hands its sum over through LDS, and kh = 0 stores the
+//     chunk's output at the start of the next chunk.
 // The A operands come straight from the fragment-ordered record (L2), the
 // B operands (S, v_new) from LDS.  blockIdx -> (item, slice) keeps the 8
 // slices of one head on one XCD (workgroups go round-robin over the 8
@@ -477,18 +490,15 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 constexpr int kXcds = 8;
 constexpr int kScanThreads = 512;
 
-// Wave w = (row tile rt = w % 4, role hf = w / 4): role 0 forms v_new rows
-// 16rt.. (k_cumdecay . S), role 1 the output rows 16rt.. ((q e^cum) . S +
-// intra . v_new); wave w then updates state rows 16w.. .  With kPrefetch
-// (more than one chunk) the operands of chunk c+1 are loaded into
-// registers while chunk c computes.
 template <bool kPrefetch>
 __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
-  __shared__ float S[kD * 20];   // state slice (dk x 16)
-  __shared__ float Vn[kC * 20];  // v_new
+  __shared__ float S[kD * 20];     // state slice (dk x 16), updated in place
+  __shared__ float Vn0[kC * 20];   // new_values - k_cumdecay . S, first half of dk
+  __shared__ float Vn1[kC * 20];   // k_cumdecay . S, second half of dk
+  __shared__ float Opart[kC * 20]; // (q e^cum) . S, second half of dk
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rt = wave & 3, hf = wave >> 2;
+  const int rt = wave & 3, kh = wave >> 2;
   constexpr int nslice = kD / kW;
   const int b = blockIdx.x;
   const int item = (b % kXcds) + kXcds * (b / (kXcds * nslice));  // (row, head) index
@@ -503,60 +513,112 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
     S[i * 20 + j] = g.s_in ? g.s_in[r * g.s_in_sb + ((int64_t)h * kD + i) * kD + col0 + j] : 0.0f;
   }
   __syncthreads();
+  // A operands of one chunk for this wave; every field is written on every
+  // path (a struct written on one branch only is kept in scratch memory).
   struct Ops {
-    f32x4 a[8], ia[4], d[4], nvv;
+    f32x4 kc[4], qd[4], kd[4], in[2], nvv;
     float decay;
   };
   auto fetch = [&](int c, Ops& o) {
     const float* rec = g.rec + ((int64_t)item * g.n_chunks + c) * kRecFloats;
-    const f32x4* ap = (const f32x4*)(rec + (hf ? kRecQd : kRecKc)) + rt * 8 * 64 + lane;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o.a[j] = ap[j * 64];
-    if (hf) {
-      const f32x4* inp = (const f32x4*)(rec + kRecIn) + rt * 4 * 64 + lane;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o.ia[j] = inp[j * 64];
-    } else {
-      o.nvv = *((const f32x4*)(rec + kRecNv) + (sl * 4 + rt) * 64 + lane);
-    }
+    const f32x4* kcp = (const f32x4*)(rec + kRecKc) + rt * 8 * 64 + 4 * kh * 64 + lane;
+    const f32x4* qdp = (const f32x4*)(rec + kRecQd) + rt * 8 * 64 + 4 * kh * 64 + lane;
     const f32x4* kdp = (const f32x4*)(rec + kRecKd) + wave * 4 * 64 + lane;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o.d[j] = kdp[j * 64];
+    for (int j = 0; j < 4; ++j) {
+      o.kc[j] = kcp[j * 64];
+      o.qd[j] = qdp[j * 64];
+      o.kd[j] = kdp[j * 64];
+    }
+    // intra blocks j = kh, kh + 2 of row tile rt
+    const f32x4* inp = (const f32x4*)(rec + kRecIn) + rt * 4 * 64 + kh * 64 + lane;
+    o.in[0] = inp[0];
+    o.in[1] = inp[2 * 64];
+    if (kh == 0) {
+      o.nvv = *((const f32x4*)(rec + kRecNv) + (sl * 4 + rt) * 64 + lane);
+    } else {
+      o.nvv = f32x4{};
+    }
     o.decay = rec[kRecDecay];
   };
-  auto chunk = [&](int c, Ops& cur, Ops& nxt) {
-    if (kPrefetch && c + 1 < g.n_chunks) fetch(c + 1, nxt);
-    // phase 1: K = dk chain against the state slice
-    f32x4v acc = {0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc = mma16(cur.a[j][e], S[(4 * (4 * j + e) + fq) * 20 + fm], acc);
-    if (!hf) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Vn[(16 * rt + 4 * fq + e) * 20 + fm] = cur.nvv[e] - acc[e];
-    }
-    __syncthreads();
-    // phase 2: intra . v_new (intra is lower triangular: K stops at the
-    // diagonal block), then this wave's 16 state rows
-    if (hf) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (j <= rt) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc = mma16(cur.ia[j][e], Vn[(4 * (4 * j + e) + fq) * 20 + fm], acc);
-        }
+  // the output of the previous chunk (kh = 0 waves): its first half and intra
+  // term in registers, the second half in Opart
+  f32x4v out_prev = {0, 0, 0, 0};
+  auto store_out = [&](int c) {
+    if (kh == 0 && c >= 0) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int t = c * kC + 16 * rt + 4 * fq + e;
-        if (t < g.t) g.core[(((int64_t)r * g.t + t) * g.nv + h) * kD + col0 + fm] = acc[e];
+        const int row = 16 * rt + 4 * fq + e;
+        const int t = c * kC + row;
+        if (t < g.t) g.core[(((int64_t)r * g.t + t) * g.nv + h) * kD + col0 + fm] = out_prev[e] + Opart[row * 20 + fm];
       }
     }
-    f32x4v su = {0, 0, 0, 0};
+  };
+  auto chunk = [&](int c, Ops& cur, Ops& nxt) {
+    store_out(c - 1);
+    // phase A: this wave's half of dk against the state slice; the 16 state
+    // operands are read before the first MFMA and reused by (q e^cum) . S
+    float sb[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sb[i] = S[(4 * (16 * kh + i) + fq) * 20 + fm];
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4v acc = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) su = mma16(cur.d[j][e], Vn[(4 * (4 * j + e) + fq) * 20 + fm], su);
+      for (int e = 0; e < 4; ++e) acc = mma16(cur.kc[j][e], sb[4 * j + e], acc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = 16 * rt + 4 * fq + e;
+      if (kh == 0)
+        Vn0[row * 20 + fm] = cur.nvv[e] - acc[e];
+      else
+        Vn1[row * 20 + fm] = acc[e];
+    }
+    // The next chunk's operands (about 139 KB per workgroup through the
+    // CU's 64 B/clk load path) are issued after this phase's MFMAs, which
+    // would otherwise queue behind them, and land during phase B.
+    // Unconditional (the last chunk fetches itself again): a branch around
+    // the loads made the compiler's wait tracking give up at the join.
+    if (kPrefetch) fetch(min(c + 1, g.n_chunks - 1), nxt);
+    __syncthreads();
+    // phase B
+    float vb[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) vb[i] = Vn0[(4 * i + fq) * 20 + fm] - Vn1[(4 * i + fq) * 20 + fm];
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4v su = {0, 0, 0, 0}, ob = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        su = mma16(cur.kd[j][e], vb[4 * j + e], su);
+        ob = mma16(cur.qd[j][e], sb[4 * j + e], ob);
+      }
+    // intra . v_new: intra is lower triangular (K stops at the diagonal
+    // block); blocks j = kh, kh + 2 go to this wave so the two halves share it
+    // (kh picks the path: a register array indexed by it would live in scratch)
+    auto intra = [&](auto kh_c) {
+      constexpr int KH = decltype(kh_c)::value;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * jj + KH;
+        if (j <= rt) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ob = mma16(cur.in[jj][e], vb[4 * (2 * jj + KH) + e], ob);
+        }
+      }
+    };
+    if (kh == 0)
+      intra(std::integral_constant<int, 0>{});
+    else
+      intra(std::integral_constant<int, 1>{});
+    if (kh == 0) {
+      out_prev = ob;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Opart[(16 * rt + 4 * fq + e) * 20 + fm] = ob[e];
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r0 = 16 * wave + 4 * fq + e;
@@ -564,12 +626,18 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
     }
     __syncthreads();
   };
-  Ops ops_a, ops_b;  // the two register sets alternate (no copy between chunks)
+  Ops ops_a, ops_b;
   fetch(0, ops_a);
   if constexpr (kPrefetch) {
-    for (int c = 0; c < g.n_chunks; c += 2) {
+    // One chunk per iteration: chunk c+1's operands load into ops_b while c
+    // computes, then move to ops_a.
+    for (int c = 0; c < g.n_chunks; ++c) {
       chunk(c, ops_a, ops_b);
-      if (c + 1 < g.n_chunks) chunk(c + 1, ops_b, ops_a);
+      // s_waitcnt vmcnt(0): the prefetch has had the whole chunk to land;
+      // with nothing pending at the loop head the compiler no longer waits
+      // for the next prefetch before the first MFMA of the next chunk
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      ops_a = ops_b;
     }
   } else {
     for (int c = 0; c < g.n_chunks; ++c) {
@@ -577,6 +645,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
       chunk(c, ops_a, ops_a);
     }
   }
+  store_out(g.n_chunks - 1);
   for (int p = tid; p < kD * kW; p += kScanThreads) {
     const int i = p / kW, j = p % kW;
     g.s_out[((int64_t)r * g.nv + h) * kD * kD + (int64_t)i * kD + col0 + j] = S[i * 20 + j];
