@@ -230,240 +230,344 @@ __global__ __launch_bounds__(256) void gdn_conv_state_kernel(GdnArgs g) {
 // prep: one workgroup (8 waves) per (row, value head, chunk).
 constexpr int kPrepThreads = 512;
 constexpr int kPrepWaves = kPrepThreads / 64;
+static_assert(kPrepWaves == 8, "the prep kernel's work split assumes 8 waves");
 
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row.  Every lane ends with the same bits:
+// each step adds two values that the partner lane adds in the other order.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f<0xB1>(x);   // lane ^ 1
+  x += dpp_f<0x4E>(x);   // lane ^ 2
+  x += dpp_f<0x141>(x);  // half-row mirror: quad 0 <-> 1, 2 <-> 3
+  x += dpp_f<0x140>(x);  // row mirror: quads {0,1} <-> {3,2}
+  return x;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct PrepLds {
+  float Qs[kC * kSX];  // q normalised * dk^-0.5; later k_cumdecay staging
+  float Ks[kC * kSX];  // k normalised
+  float Us[kC * kSC];  // ut, strict lower (tiles at and below the diagonal)
+  float Iv[kC * kSC];  // (I + ut)^-1 (tiles at and below the diagonal)
+  float Tm[kC * kSC];  // products of the block inversion
+  float In[kC * kSC];  // intra tiles on their way to record order
+  float betas[kC], cums[kC], ecum[kC], ekd[kC];
+};
+
+// One 16x16 tile (ti, tj), tj <= ti, of G = (k beta) k^T (DG) and / or
+// QK = q k^T (DQ).  The k-sum runs in the order 16j + 4fq + e, so each lane
+// reads its A and B operands as 16-byte vectors.  Epilogue:
+//   ut[i][j] = G[i][j] pair[i][j] for j < i,   pair = e^(cum_i - cum_j),
+//   intra[i][j] = QK[i][j] pair[i][j] for j <= i  (qwen35.rs:318-330),
+// ut into Us; intra through the wave's own In tile into its record order.
+template <bool DG, bool DQ>
+__device__ __forceinline__ void prep_tile(PrepLds& L, float* rec, int ti, int tj, int lane) {
+  const int fm = lane & 15, fq = lane >> 4;
+  const float* ka = L.Ks + (16 * ti + fm) * kSX + 4 * fq;
+  const float* qa = L.Qs + (16 * ti + fm) * kSX + 4 * fq;
+  const float* kb = L.Ks + (16 * tj + fm) * kSX + 4 * fq;
+  const float bi = DG ? L.betas[16 * ti + fm] : 0.0f;
+  f32x4v gacc = {0, 0, 0, 0}, qacc = {0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < kD / 16; ++j) {
+    const f32x4 b4 = *(const f32x4*)(kb + 16 * j);
+    f32x4 a4 = {0, 0, 0, 0}, q4 = {0, 0, 0, 0};
+    if (DG) a4 = *(const f32x4*)(ka + 16 * j);
+    if (DQ) q4 = *(const f32x4*)(qa + 16 * j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (DG) gacc = mma16(a4[e] * bi, b4[e], gacc);
+      if (DQ) qacc = mma16(q4[e], b4[e], qacc);
+    }
+  }
+  const int j = 16 * tj + fm;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = 16 * ti + 4 * fq + e;
+    const float pair = j <= i ? expf(L.cums[i] - L.cums[j]) : 0.0f;
+    if (DG) L.Us[i * kSC + j] = j < i ? gacc[e] * pair : 0.0f;
+    if (DQ) L.In[i * kSC + j] = qacc[e] * pair;
+  }
+  if (DQ) {
+    wave_lds_sync();
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = L.In[(16 * ti + fm) * kSC + 16 * tj + 4 * e + fq];
+    *(f32x4*)(rec + kRecIn + 4 * ((ti * 4 + tj) * 64 + lane)) = v;
+  }
+}
+
+// 16x16 diagonal block b of inv = (I + L)^-1, L = Us strict lower, by
+// forward substitution: lane j (of each 16-lane group) owns column j,
+//   inv[i][j] = -sum_{k<i} L[i][k] inv[k][j]  (inv[k][j] = 0 for k < j,
+//   1 for k == j); the L[i][k] reads are broadcasts.  Lanes with fq == 0 write.
+__device__ __forceinline__ void prep_inv16(PrepLds& L, int b, int lane) {
+  const int b0 = 16 * b, j = lane & 15;
+  float col[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) col[k] = k == j ? 1.0f : 0.0f;
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    const float* Lrow = L.Us + (b0 + i) * kSC + b0;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < i; ++k) acc += Lrow[k] * col[k];
+    col[i] = i > j ? -acc : col[i];
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) L.Iv[(b0 + i) * kSC + b0 + j] = col[i];
+  }
+}
+
+// Work split (8 waves, wave w on SIMD w % 4; every SIMD gets 5 tile products):
+//   load   all:  v column slice 16w.. into registers, q / k rows l2-normed
+//                into LDS; wave 0: gates, cum (sequential, as the reference)
+//   tiles  w 0-2: two off-diagonal tiles, both products; w 3: the four
+//                diagonal QK products; w 4 + b: the diagonal G product of
+//                block b, its 16x16 inverse, then the Qd / Kd records and
+//                the zero tiles of intra
+//   inv    32-level (w 0, 1), 64-level (w 0-3); the others scale their
+//                nv / kc operands meanwhile
+//   nv/kc  wave w: column tile w of new_values and k_cumdecay, row tiles 0-3
 template <typename T>
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
-  __shared__ float Qs[kC * kSX];
-  __shared__ float Ks[kC * kSX];
-  __shared__ float Vs[kC * kSX];
-  __shared__ float Us[kC * kSC];   // strict lower ut
-  __shared__ float Iv[kC * kSC];   // (I + Us)^-1
-  __shared__ float Tm[kC * kSC];   // products of the block inversion
-  __shared__ float gs[kC], betas[kC], cums[kC], ecum[kC], ekd[kC];
-
+  __shared__ PrepLds L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fm = lane & 15, fq = lane >> 4;  // fragment row / k-slot of this lane
   const int c = blockIdx.x % g.n_chunks;
   const int hr = blockIdx.x / g.n_chunks;
   const int h = hr % g.nv, r = hr / g.nv;
   const int kh = h / (g.nv / g.nk);  // value head h reads key head h / (nv/nk) (qwen35.rs:436-442)
   const int key_dim = g.nk * kD;
   const int t0 = c * kC;
-
-  // ---- load q, k, v of the chunk (rows past t are the zero padding)
   const T* cv = (const T*)g.conved + (int64_t)r * g.t * g.conv_dim;
-  for (int p = tid; p < kC * (kD / 8); p += kPrepThreads) {
-    const int i = p / (kD / 8), col = (p % (kD / 8)) * 8;
-    const int t = t0 + i;
-    float qv[8], kv[8], vv[8];
-    if (t < g.t) {
-      const T* row = cv + (int64_t)t * g.conv_dim;
-      load8<T>(row + kh * kD + col, qv);
-      load8<T>(row + key_dim + kh * kD + col, kv);
-      load8<T>(row + 2 * key_dim + h * kD + col, vv);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qv[e] = kv[e] = vv[e] = 0.0f;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      Qs[i * kSX + col + e] = qv[e];
-      Ks[i * kSX + col + e] = kv[e];
-      Vs[i * kSX + col + e] = vv[e];
-    }
-  }
-  if (tid < kC) {
-    const int t = t0 + tid;
-    float gv = 0.0f, bv = 0.0f;
-    if (t < g.t) {
-      const float av = to_f(((const T*)g.a)[r * g.ab_sb + (int64_t)t * g.ab_st + h]);
-      const float bb = to_f(((const T*)g.b)[r * g.ab_sb + (int64_t)t * g.ab_st + h]);
-      const float x = av + g.dt_bias[h];
-      const float sp = fmaxf(x, 0.0f) + logf(expf(-fabsf(x)) + 1.0f);  // softplus (qwen35.rs:243-248)
-      gv = sp * g.neg_a[h];
-      bv = 1.0f / (1.0f + expf(-bb));
-    }
-    gs[tid] = gv;
-    betas[tid] = bv;
-  }
-  __syncthreads();
-
-  // ---- l2norm of q (then * dk^-0.5) and k rows: wave w takes rows w, w+8, ...
-  const float qscale = 0.08838834764831845f;  // 128^-0.5
-  for (int i = wave; i < 2 * kC; i += kPrepWaves) {
-    float* row = i < kC ? Qs + i * kSX : Ks + (i - kC) * kSX;
-    const float x0 = row[lane], x1 = row[lane + 64];
-    float s = x0 * x0 + x1 * x1;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    const float n = sqrtf(s + 1e-6f);
-    const float sc = i < kC ? qscale : 1.0f;
-    row[lane] = x0 / n * sc;
-    row[lane + 64] = x1 / n * sc;
-  }
-  if (tid == 0) {
-    float acc = 0.0f;
-    for (int i = 0; i < kC; ++i) {
-      acc += gs[i];
-      cums[i] = acc;
-    }
-  }
-  __syncthreads();
-  if (tid < kC) {
-    ecum[tid] = expf(cums[tid]);
-    ekd[tid] = expf(cums[kC - 1] - cums[tid]);
-  }
-
   float* rec = g.rec + (int64_t)blockIdx.x * kRecFloats;
-  const int fm = lane & 15, fq = lane >> 4;  // fragment row / k-slot of this lane
 
-  // ---- G = K K^T and QK = Q K^T on the 16x16 tiles; ut, intra.  The 10
-  // lower tiles come first in the order below so the waves share them
-  // evenly; the 6 upper tiles only write zeros.
-  for (int tile = wave; tile < 16; tile += kPrepWaves) {
-    constexpr int kOrder[16][2] = {{0, 0}, {1, 0}, {1, 1}, {2, 0}, {2, 1}, {2, 2}, {3, 0}, {3, 1},
-                                   {3, 2}, {3, 3}, {0, 1}, {0, 2}, {0, 3}, {1, 2}, {1, 3}, {2, 3}};
-    const int ti = kOrder[tile][0], tj = kOrder[tile][1];
-    f32x4v gacc = {0, 0, 0, 0}, qacc = {0, 0, 0, 0};
-    if (tj <= ti) {
-      for (int k = 0; k < kD; k += 4) {
-        const float bk = Ks[(16 * tj + fm) * kSX + k + fq];
-        gacc = mma16(Ks[(16 * ti + fm) * kSX + k + fq], bk, gacc);
-        qacc = mma16(Qs[(16 * ti + fm) * kSX + k + fq], bk, qacc);
+  // All loads below read a valid row (clamped to the last token) and the
+  // rows past t are zeroed afterwards, so no load sits behind a branch and
+  // all of them are in flight together.
+  const int t_last = g.t - 1;
+  // ---- v column slice of this wave, in the nv k order:
+  // vreg[4jg + e] = v[16jg + 4fq + e][16 wave + fm] (rows past t are zero)
+  float vreg[16], kreg[16];
+  {
+    const T* vcol = cv + 2 * key_dim + h * kD + 16 * wave + fm;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int t = t0 + 16 * (x >> 2) + 4 * fq + (x & 3);
+      const float v = to_f(vcol[(int64_t)min(t, t_last) * g.conv_dim]);
+      vreg[x] = t < g.t ? v : 0.0f;
+    }
+  }
+  // ---- q, k rows i and i + 32, 16 lanes per row, 8 columns each; l2norm
+  // x / sqrt(sum x^2 + 1e-6), q then * dk^-0.5 (qwen35.rs:250-254, :305-306)
+  {
+    const int i0 = tid >> 4, col = (tid & 15) * 8;
+    float qv[2][8], kv[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + i0 + 32 * u;
+      const T* row = cv + (int64_t)min(t, t_last) * g.conv_dim;
+      load8<T>(row + kh * kD + col, qv[u]);
+      load8<T>(row + key_dim + kh * kD + col, kv[u]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qv[u][e] = t < g.t ? qv[u][e] : 0.0f;
+        kv[u][e] = t < g.t ? kv[u][e] : 0.0f;
       }
     }
+    const float qscale = 0.08838834764831845f;  // 128^-0.5
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * ti + 4 * fq + e, j = 16 * tj + fm;
-      const float pair = j <= i ? expf(cums[i] - cums[j]) : 0.0f;
-      Us[i * kSC + j] = j < i ? betas[i] * gacc[e] * pair : 0.0f;
-      Tm[i * kSC + j] = qacc[e] * pair;  // intra
+    for (int u = 0; u < 2; ++u) {
+      float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sq += qv[u][e] * qv[u][e];
+        sk += kv[u][e] * kv[u][e];
+      }
+      const float nq = sqrtf(row16_sum(sq) + 1e-6f), nk = sqrtf(row16_sum(sk) + 1e-6f);
+      float* qrow = L.Qs + (i0 + 32 * u) * kSX + col;
+      float* krow = L.Ks + (i0 + 32 * u) * kSX + col;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        f32x4 a, b;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a[e] = qv[u][4 * hf + e] / nq * qscale;
+          b[e] = kv[u][4 * hf + e] / nk;
+        }
+        *(f32x4*)(qrow + 4 * hf) = a;
+        *(f32x4*)(krow + 4 * hf) = b;
+      }
     }
   }
-  __syncthreads();
-  // intra in A-fragment order: [w 4][j 4][lane][4]
-  for (int p = tid; p < kC * kC / 4; p += kPrepThreads) {
-    const int l = p & 63, j = (p >> 6) & 3, w = p >> 8;
-    f32x4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = Tm[(16 * w + (l & 15)) * kSC + 4 * (4 * j + e) + (l >> 4)];
-    *(f32x4*)(rec + kRecIn + 4 * p) = v;
-  }
-  // q e^cum and k e^(last - cum) in their fragment orders; e^last
-  for (int p = tid; p < kC * kD / 4; p += kPrepThreads) {
-    const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;       // Qd: [w 4][j 8][lane]
-    f32x4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * w + (l & 15), k = 4 * (4 * j + e) + (l >> 4);
-      v[e] = Qs[i * kSX + k] * ecum[i];
-    }
-    *(f32x4*)(rec + kRecQd + 4 * p) = v;
-    const int jj = (p >> 6) & 3, ti = p >> 8;                  // Kd: [ti 8][j 4][lane]
-    f32x4 u;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 4 * (4 * jj + e) + (l >> 4), col = 16 * ti + (l & 15);
-      u[e] = Ks[i * kSX + col] * ekd[i];
-    }
-    *(f32x4*)(rec + kRecKd + 4 * p) = u;
-  }
-  if (tid == 0) rec[kRecDecay] = expf(cums[kC - 1]);
-  __syncthreads();  // Tm is reused by the inversion
-
-  // ---- inv = (I + L)^-1, L = Us strict lower, by the block recursion of
-  // inv_unit_lower (qwen35.rs:277-296) over 16, 32, 64:
-  //   [A 0; C B]^-1 = [A^-1 0; -(B^-1 C) A^-1  B^-1].
-  // 16x16 diagonal blocks by forward substitution, all four in wave 0:
-  // lane 16b + j owns column j of block b in registers,
-  //   inv[i][j] = -sum_{k<i} L[i][k] inv[k][j]  (inv[k][j] = 0 for k < j,
-  //   1 for k == j), the L[i][k] reads being wave-wide broadcasts per block.
+  // ---- gates (lane = chunk row): beta = sigmoid(b), g = softplus(a +
+  // dt_bias) * -e^A (qwen35.rs:243-248, :436-440); cum = running sum of g in
+  // row order (lane i adds g_0 .. g_i one by one, like the reference)
   if (wave == 0) {
-    const int b0 = 16 * (lane >> 4), j = lane & 15;
-    float col[16];
+    const int t = t0 + lane;
+    const int64_t ab = r * g.ab_sb + (int64_t)min(t, t_last) * g.ab_st + h;
+    const float av = to_f(((const T*)g.a)[ab]);
+    const float bb = to_f(((const T*)g.b)[ab]);
+    const float x = av + g.dt_bias[h];
+    const float sp = fmaxf(x, 0.0f) + logf(expf(-fabsf(x)) + 1.0f);
+    const float gv = t < g.t ? sp * g.neg_a[h] : 0.0f;
+    const float bv = t < g.t ? 1.0f / (1.0f + expf(-bb)) : 0.0f;
+    float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) col[k] = k == j ? 1.0f : 0.0f;
-#pragma unroll
-    for (int i = 1; i < 16; ++i) {
-      const float* Lrow = Us + (b0 + i) * kSC + b0;
-      float acc = 0.0f;
-#pragma unroll
-      for (int k = 0; k < i; ++k) acc += Lrow[k] * col[k];
-      col[i] = i > j ? -acc : col[i];
+    for (int k = 0; k < kC; ++k) {
+      const float gk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gv), k));
+      const float s = acc + gk;
+      acc = k <= lane ? s : acc;
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) Iv[(b0 + i) * kSC + b0 + j] = col[i];
+    const float last = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), kC - 1));
+    L.betas[lane] = bv;
+    L.cums[lane] = acc;
+    L.ecum[lane] = expf(acc);
+    L.ekd[lane] = expf(last - acc);
+    if (lane == 0) rec[kRecDecay] = expf(last);
   }
   __syncthreads();
-  // 32x32 level: blocks [0,32) (wave 0) and [32,64) (wave 1): off-diagonal
-  // 16x16 block = -(B^-1 C) A^-1.
+
+  // ---- G / QK tiles, the 16x16 diagonal inverses, the Qd / Kd records
+  if (wave < 3) {
+    constexpr int kOff[3][2][2] = {{{1, 0}, {2, 0}}, {{2, 1}, {3, 0}}, {{3, 1}, {3, 2}}};
+    prep_tile<true, true>(L, rec, kOff[wave][0][0], kOff[wave][0][1], lane);
+    prep_tile<true, true>(L, rec, kOff[wave][1][0], kOff[wave][1][1], lane);
+  } else if (wave == 3) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) prep_tile<false, true>(L, rec, b, b, lane);
+  } else {
+    const int b = wave - 4;
+    prep_tile<true, false>(L, rec, b, b, lane);
+    wave_lds_sync();
+    prep_inv16(L, b, lane);
+    // q e^cum and k e^(last - cum) in their fragment orders
+    const int t4 = tid - 256;
+    for (int p = t4; p < kC * kD / 4; p += 256) {
+      const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;  // Qd: [w 4][j 8][lane]
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 16 * w + (l & 15), k = 4 * (4 * j + e) + (l >> 4);
+        v[e] = L.Qs[i * kSX + k] * L.ecum[i];
+      }
+      *(f32x4*)(rec + kRecQd + 4 * p) = v;
+      const int jj = (p >> 6) & 3, ti = p >> 8;  // Kd: [ti 8][j 4][lane]
+      f32x4 u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 4 * (4 * jj + e) + (l >> 4), col = 16 * ti + (l & 15);
+        u[e] = L.Ks[i * kSX + col] * L.ekd[i];
+      }
+      *(f32x4*)(rec + kRecKd + 4 * p) = u;
+    }
+    // intra's six tiles above the diagonal are zero
+    constexpr int kUp[6] = {1, 2, 3, 6, 7, 11};  // ti * 4 + tj, tj > ti
+    for (int p = t4; p < 6 * 64; p += 256)
+      *(f32x4*)(rec + kRecIn + 4 * (kUp[p >> 6] * 64 + (p & 63))) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  __syncthreads();
+
+  // nv / kc operands of this wave's column tile: v beta, (k beta) e^cum
+  // (qwen35.rs:309-312, :336-340), in the same k order as vreg
+  auto operands = [&]() {
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      const f32x4 b4 = *(const f32x4*)(L.betas + 16 * jg + 4 * fq);
+      const f32x4 e4 = *(const f32x4*)(L.ecum + 16 * jg + 4 * fq);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 16 * jg + 4 * fq + e;
+        vreg[4 * jg + e] = vreg[4 * jg + e] * b4[e];
+        kreg[4 * jg + e] = (L.Ks[i * kSX + 16 * wave + fm] * b4[e]) * e4[e];
+      }
+    }
+  };
+
+  // ---- inverse, 32x32 level: blocks [0,32) (wave 0) and [32,64) (wave 1),
+  // off-diagonal 16x16 block = -(B^-1 C) A^-1 (the split of
+  // inv_unit_lower, qwen35.rs:277-296)
   if (wave < 2) {
-    const int o = 32 * wave;  // block origin
-    const float* Ainv = Iv + o * kSC + o;                  // rows o..o+15, cols o..o+15
-    const float* Binv = Iv + (o + 16) * kSC + o + 16;      // rows o+16.., cols o+16..
-    const float* Cb = Us + (o + 16) * kSC + o;             // rows o+16.., cols o..
+    const int o = 32 * wave;
+    const float* Ainv = L.Iv + o * kSC + o;
+    const float* Binv = L.Iv + (o + 16) * kSC + o + 16;
+    const float* Cb = L.Us + (o + 16) * kSC + o;
     f32x4v bc = {0, 0, 0, 0};
+#pragma unroll
     for (int k = 0; k < 16; k += 4) bc = mma16(Binv[fm * kSC + k + fq], Cb[(k + fq) * kSC + fm], bc);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Tm[(o + 4 * fq + e) * kSC + fm] = bc[e];  // B^-1 C, rows 0..15 of the block
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    for (int e = 0; e < 4; ++e) L.Tm[(o + 4 * fq + e) * kSC + fm] = bc[e];
+    wave_lds_sync();
     f32x4v x = {0, 0, 0, 0};
-    for (int k = 0; k < 16; k += 4) x = mma16(Tm[(o + fm) * kSC + k + fq], Ainv[(k + fq) * kSC + fm], x);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Iv[(o + 16 + 4 * fq + e) * kSC + o + fm] = -x[e];
-    // the upper off-diagonal block stays zero
-    for (int e = 0; e < 4; ++e) Iv[(o + 4 * fq + e) * kSC + o + 16 + fm] = 0.0f;
+    for (int k = 0; k < 16; k += 4) x = mma16(L.Tm[(o + fm) * kSC + k + fq], Ainv[(k + fq) * kSC + fm], x);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) L.Iv[(o + 16 + 4 * fq + e) * kSC + o + fm] = -x[e];
   }
+  operands();
   __syncthreads();
-  // 64x64 level: off block (rows 32..63, cols 0..31) = -(B^-1 C) A^-1 with
-  // 32x32 A^-1 = Iv[0:32,0:32], B^-1 = Iv[32:64,32:64], C = Us[32:64,0:32].
-  // Wave w < 4 computes the 16x16 tile (w/2, w%2) of B^-1 C, then of the product.
+  // ---- 64x64 level: off block (rows 32..63, cols 0..31) = -(B^-1 C) A^-1
+  // with A^-1 = Iv[0:32, 0:32], B^-1 = Iv[32:64, 32:64], C = Us[32:64, 0:32];
+  // wave w < 4 takes the 16x16 tile (w / 2, w % 2) of each product.  Both
+  // inverses are lower triangular, so the k range of tile row ti stops at
+  // 16 (ti + 1) in B^-1 C and starts at 16 tj in the product with A^-1.
+  const int ti2 = (wave >> 1) & 1, tj2 = wave & 1;
   if (wave < 4) {
-    const int ti = wave >> 1, tj = wave & 1;
     f32x4v bc = {0, 0, 0, 0};
-    for (int k = 0; k < 32; k += 4)
-      bc = mma16(Iv[(32 + 16 * ti + fm) * kSC + 32 + k + fq], Us[(32 + k + fq) * kSC + 16 * tj + fm], bc);
+    for (int k = 0; k < 16 * (ti2 + 1); k += 4)
+      bc = mma16(L.Iv[(32 + 16 * ti2 + fm) * kSC + 32 + k + fq], L.Us[(32 + k + fq) * kSC + 16 * tj2 + fm], bc);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Tm[(16 * ti + 4 * fq + e) * kSC + 16 * tj + fm] = bc[e];
+    for (int e = 0; e < 4; ++e) L.Tm[(16 * ti2 + 4 * fq + e) * kSC + 16 * tj2 + fm] = bc[e];
   }
   __syncthreads();
   if (wave < 4) {
-    const int ti = wave >> 1, tj = wave & 1;
     f32x4v x = {0, 0, 0, 0};
-    for (int k = 0; k < 32; k += 4) x = mma16(Tm[(16 * ti + fm) * kSC + k + fq], Iv[(k + fq) * kSC + 16 * tj + fm], x);
+    for (int k = 16 * tj2; k < 32; k += 4)
+      x = mma16(L.Tm[(16 * ti2 + fm) * kSC + k + fq], L.Iv[(k + fq) * kSC + 16 * tj2 + fm], x);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Iv[(32 + 16 * ti + 4 * fq + e) * kSC + 16 * tj + fm] = -x[e];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) Iv[(16 * ti + 4 * fq + e) * kSC + 32 + 16 * tj + fm] = 0.0f;
+    for (int e = 0; e < 4; ++e) L.Iv[(32 + 16 * ti2 + 4 * fq + e) * kSC + 16 * tj2 + fm] = -x[e];
   }
   __syncthreads();
 
-  // ---- new_values = inv (v beta), k_cumdecay = inv (k beta e^cum):
-  // 4 x 8 output tiles each; the K range of row tile ti stops at its
-  // diagonal block (inv is lower triangular).  new_values goes out in the
-  // scan's accumulator order; k_cumdecay is staged in Qs (free now) and
-  // written in A-fragment order.
-  for (int tile = wave; tile < 32; tile += kPrepWaves) {
-    const int ti = tile / 8, tn = tile % 8;
-    f32x4v nv = {0, 0, 0, 0}, kc = {0, 0, 0, 0};
-    for (int k = 0; k < 16 * (ti + 1); k += 4) {
-      const float av = Iv[(16 * ti + fm) * kSC + k + fq];
-      const int kk = k + fq;
-      const float bsc = betas[kk];
-      nv = mma16(av, Vs[kk * kSX + 16 * tn + fm] * bsc, nv);
-      kc = mma16(av, Ks[kk * kSX + 16 * tn + fm] * (bsc * ecum[kk]), kc);
-    }
-    *(f32x4*)(rec + kRecNv + ((tn * 4 + ti) * 64 + lane) * 4) = f32x4{nv[0], nv[1], nv[2], nv[3]};
+  // ---- new_values = inv (v beta), k_cumdecay = inv (k beta e^cum) for the
+  // row tiles ti of this wave's column tile; inv is lower triangular, so
+  // row tile ti sums over k < 16 (ti + 1).  new_values goes out in the
+  // scan's accumulator order; k_cumdecay through this wave's columns of Qs
+  // (free now) into A-fragment order.
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Qs[(16 * ti + 4 * fq + e) * kSX + 16 * tn + fm] = kc[e];
+  for (int ti = 0; ti < 4; ++ti) {
+    f32x4v nv = {0, 0, 0, 0}, kc = {0, 0, 0, 0};
+#pragma unroll
+    for (int jg = 0; jg <= ti; ++jg) {
+      const f32x4 a4 = *(const f32x4*)(L.Iv + (16 * ti + fm) * kSC + 16 * jg + 4 * fq);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        nv = mma16(a4[e], vreg[4 * jg + e], nv);
+        kc = mma16(a4[e], kreg[4 * jg + e], kc);
+      }
+    }
+    *(f32x4*)(rec + kRecNv + ((wave * 4 + ti) * 64 + lane) * 4) = f32x4{nv[0], nv[1], nv[2], nv[3]};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) L.Qs[(16 * ti + 4 * fq + e) * kSX + 16 * wave + fm] = kc[e];
   }
-  __syncthreads();
-  for (int p = tid; p < kC * kD / 4; p += kPrepThreads) {
-    const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;
+  wave_lds_sync();
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti) {
     f32x4 v;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = Qs[(16 * w + (l & 15)) * kSX + 4 * (4 * j + e) + (l >> 4)];
-    *(f32x4*)(rec + kRecKc + 4 * p) = v;
+    for (int e = 0; e < 4; ++e) v[e] = L.Qs[(16 * ti + fm) * kSX + 16 * wave + 4 * e + fq];
+    *(f32x4*)(rec + kRecKc + 4 * ((ti * 8 + wave) * 64 + lane)) = v;
   }
 }
 
