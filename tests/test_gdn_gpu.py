@@ -90,6 +90,39 @@ def test_gdn_carried_state_vs_oracle(gpu, orc, bf16):
     assert ey <= (BF16_TOL if bf16 else F32_TOL)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gdn_strided_views_vs_oracle(gpu, orc, bf16):
+    """z as a column slice of a wider tensor (odd row stride, a view into a
+    fused projection output) and y written into such a view: the
+    element-wise norm path.  mixed with rows that are not 16-byte aligned is
+    refused (the conv reads 8-element vectors)."""
+    import torch
+    w = configs.GdnWorkload("gdn-strided", 13, bf16, 2, 70, nk=2, nv=4)
+    inp = w.inputs()
+    dt = torch.bfloat16 if bf16 else torch.float32
+    wide = lambda x: torch.cat([torch.zeros(x.shape[:-1] + (1,), dtype=dt, device=gpu), to_dev(np.ascontiguousarray(x), bf16, gpu)], -1)
+    mixed = to_dev(inp["mixed"], bf16, gpu)
+    z = wide(inp["z"])[..., 1:]
+    assert z.stride(1) % 2 == 1
+    f32 = lambda x: torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu)
+    layer = cev_hip.GatedDeltaNet(w.batch, w.t, w.nk, w.nv, w.dk, w.dv, w.kernel, w.eps, dtype=dt, device=gpu)
+    y_wide = torch.zeros(w.batch, w.t, w.nv * w.dv + 3, dtype=dt, device=gpu)
+    y, co, so = layer(mixed, z, to_dev(inp["b"], bf16, gpu), to_dev(inp["a"], bf16, gpu), to_dev(inp["conv_w"], bf16, gpu),
+                      f32(inp["neg_a"]), f32(inp["dt_bias"]), f32(inp["norm_w"]), y=y_wide[..., 3:])
+    torch.cuda.synchronize()
+    ry, rco, rso = _run_oracle(orc, w, inp)
+    ey = float(np.abs(to_np(y) - ry).max())
+    es = float(np.abs(to_np(so) - rso).max())
+    _say(f"gdn strided views bf16={bf16}: max|d| y {ey:.3g} state {es:.3g}")
+    assert np.array_equal(to_np(co), rco)
+    assert es <= F32_TOL
+    assert ey <= (BF16_TOL if bf16 else F32_TOL)
+    assert not to_np(y_wide[..., :3]).any()
+    with pytest.raises(cev_hip.CevError, match="8-element aligned"):
+        layer(wide(inp["mixed"])[..., 1:], z, to_dev(inp["b"], bf16, gpu), to_dev(inp["a"], bf16, gpu),
+              to_dev(inp["conv_w"], bf16, gpu), f32(inp["neg_a"]), f32(inp["dt_bias"]), f32(inp["norm_w"]))
+
+
 def test_gdn_c5_heads_vs_oracle(gpu, orc):
     """Config 5's head layout (Hk 16 -> Hv 32) on the first 256 tokens."""
     w = configs.c5_gdn(t=256)
