@@ -253,7 +253,7 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-struct PrepLds {
+struct __attribute__((aligned(16))) PrepLds {
   float Qs[kC * kSX];  // q normalised * dk^-0.5; later k_cumdecay staging
   float Ks[kC * kSX];  // k normalised
   float Us[kC * kSC];  // ut, strict lower (tiles at and below the diagonal)
@@ -334,10 +334,10 @@ __device__ __forceinline__ void prep_inv16(PrepLds& L, int b, int lane) {
 //                into LDS; wave 0: gates, cum (sequential, as the reference)
 //   tiles  w 0-2: two off-diagonal tiles, both products; w 3: the four
 //                diagonal QK products; w 4 + b: the diagonal G product of
-//                block b, its 16x16 inverse, then the Qd / Kd records and
-//                the zero tiles of intra
-//   inv    32-level (w 0, 1), 64-level (w 0-3); the others scale their
-//                nv / kc operands meanwhile
+//                block b and its 16x16 inverse
+//   inv    32-level (w 0, 1; w 2-7 write the Qd records), 64-level (w 0-3;
+//                w 4-7 write the Kd records and intra's zero tiles); every
+//                wave scales its nv / kc operands after the 32-level
 //   nv/kc  wave w: column tile w of new_values and k_cumdecay, row tiles 0-3
 template <typename T>
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
@@ -439,11 +439,24 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   }
   __syncthreads();
 
-  // ---- G / QK tiles, the 16x16 diagonal inverses, the Qd / Kd records
+  // v beta for the nv operands: done before this wave issues any store, so
+  // the wait for the v loads waits for nothing else
+#pragma unroll
+  for (int jg = 0; jg < 4; ++jg) {
+    const f32x4 b4 = *(const f32x4*)(L.betas + 16 * jg + 4 * fq);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vreg[4 * jg + e] = vreg[4 * jg + e] * b4[e];
+  }
+#pragma unroll
+  for (int x = 0; x < 16; ++x) asm volatile("" : "+v"(vreg[x]));  // keeps the compiler from sinking it
+
+  // ---- G / QK tiles and the 16x16 diagonal inverses
+  // (Tile indices by arithmetic: a table indexed by wave would be a global
+  // load, and its wait would also wait for this wave's record stores.)
   if (wave < 3) {
-    constexpr int kOff[3][2][2] = {{{1, 0}, {2, 0}}, {{2, 1}, {3, 0}}, {{3, 1}, {3, 2}}};
-    prep_tile<true, true>(L, rec, kOff[wave][0][0], kOff[wave][0][1], lane);
-    prep_tile<true, true>(L, rec, kOff[wave][1][0], kOff[wave][1][1], lane);
+    // wave 0: (1,0) (2,0); wave 1: (2,1) (3,0); wave 2: (3,1) (3,2)
+    prep_tile<true, true>(L, rec, wave == 0 ? 1 : wave + 1, wave == 0 ? 0 : 1, lane);
+    prep_tile<true, true>(L, rec, wave == 0 ? 2 : 3, wave == 2 ? 2 : 0, lane);
   } else if (wave == 3) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) prep_tile<false, true>(L, rec, b, b, lane);
@@ -452,10 +465,14 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
     prep_tile<true, false>(L, rec, b, b, lane);
     wave_lds_sync();
     prep_inv16(L, b, lane);
-    // q e^cum and k e^(last - cum) in their fragment orders
-    const int t4 = tid - 256;
-    for (int p = t4; p < kC * kD / 4; p += 256) {
-      const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;  // Qd: [w 4][j 8][lane]
+  }
+  __syncthreads();
+
+  // Records the inversion's idle waves write: q e^cum (Qd) and k e^(last -
+  // cum) (Kd) in their fragment orders, and intra's six zero tiles.
+  auto qd_records = [&](int p0, int step) {
+    for (int p = p0; p < kC * kD / 4; p += step) {
+      const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;  // [w 4][j 8][lane]
       f32x4 v;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -463,7 +480,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
         v[e] = L.Qs[i * kSX + k] * L.ecum[i];
       }
       *(f32x4*)(rec + kRecQd + 4 * p) = v;
-      const int jj = (p >> 6) & 3, ti = p >> 8;  // Kd: [ti 8][j 4][lane]
+    }
+  };
+  auto kd_records = [&](int p0, int p_end, int step) {
+    for (int p = p0; p < p_end; p += step) {
+      const int l = p & 63, jj = (p >> 6) & 3, ti = p >> 8;  // [ti 8][j 4][lane]
       f32x4 u;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -472,14 +493,16 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
       }
       *(f32x4*)(rec + kRecKd + 4 * p) = u;
     }
-    // intra's six tiles above the diagonal are zero
-    constexpr int kUp[6] = {1, 2, 3, 6, 7, 11};  // ti * 4 + tj, tj > ti
-    for (int p = t4; p < 6 * 64; p += 256)
-      *(f32x4*)(rec + kRecIn + 4 * (kUp[p >> 6] * 64 + (p & 63))) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-  __syncthreads();
+  };
+  auto zero_intra = [&](int p0, int step) {
+    for (int p = p0; p < 6 * 64; p += step) {
+      const int q = p >> 6;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+      const int ti = q < 3 ? 0 : (q < 5 ? 1 : 2), tj = q < 3 ? q + 1 : (q < 5 ? q - 1 : 3);
+      *(f32x4*)(rec + kRecIn + 4 * ((ti * 4 + tj) * 64 + (p & 63))) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
 
-  // nv / kc operands of this wave's column tile: v beta, (k beta) e^cum
+  // kc operands of this wave's column tile: (k beta) e^cum
   // (qwen35.rs:309-312, :336-340), in the same k order as vreg
   auto operands = [&]() {
 #pragma unroll
@@ -489,7 +512,6 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 16 * jg + 4 * fq + e;
-        vreg[4 * jg + e] = vreg[4 * jg + e] * b4[e];
         kreg[4 * jg + e] = (L.Ks[i * kSX + 16 * wave + fm] * b4[e]) * e4[e];
       }
     }
@@ -514,6 +536,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
     for (int k = 0; k < 16; k += 4) x = mma16(L.Tm[(o + fm) * kSC + k + fq], Ainv[(k + fq) * kSC + fm], x);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.Iv[(o + 16 + 4 * fq + e) * kSC + o + fm] = -x[e];
+  } else {
+    qd_records(tid - 128, 384);
   }
   operands();
   __syncthreads();
@@ -529,6 +553,9 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
       bc = mma16(L.Iv[(32 + 16 * ti2 + fm) * kSC + 32 + k + fq], L.Us[(32 + k + fq) * kSC + 16 * tj2 + fm], bc);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.Tm[(16 * ti2 + 4 * fq + e) * kSC + 16 * tj2 + fm] = bc[e];
+  } else {
+    kd_records(tid - 256, kC * kD / 8, 256);
+    zero_intra(tid - 256, 256);
   }
   __syncthreads();
   if (wave < 4) {
@@ -537,6 +564,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
       x = mma16(L.Tm[(16 * ti2 + fm) * kSC + k + fq], L.Iv[(k + fq) * kSC + 16 * tj2 + fm], x);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.Iv[(32 + 16 * ti2 + 4 * fq + e) * kSC + 16 * tj2 + fm] = -x[e];
+  } else {
+    kd_records(kC * kD / 8 + tid - 256, kC * kD / 4, 256);
   }
   __syncthreads();
 
@@ -548,13 +577,16 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
     f32x4v nv = {0, 0, 0, 0}, kc = {0, 0, 0, 0};
+    f32x4 a4[4];  // the row tile's inv operands, read before its MFMAs
+#pragma unroll
+    for (int jg = 0; jg <= ti; ++jg) a4[jg] = *(const f32x4*)(L.Iv + (16 * ti + fm) * kSC + 16 * jg + 4 * fq);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int jg = 0; jg <= ti; ++jg) {
-      const f32x4 a4 = *(const f32x4*)(L.Iv + (16 * ti + fm) * kSC + 16 * jg + 4 * fq);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        nv = mma16(a4[e], vreg[4 * jg + e], nv);
-        kc = mma16(a4[e], kreg[4 * jg + e], kc);
+        nv = mma16(a4[jg][e], vreg[4 * jg + e], nv);
+        kc = mma16(a4[jg][e], kreg[4 * jg + e], kc);
       }
     }
     *(f32x4*)(rec + kRecNv + ((wave * 4 + ti) * 64 + lane) * 4) = f32x4{nv[0], nv[1], nv[2], nv[3]};
