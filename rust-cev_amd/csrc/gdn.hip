@@ -627,7 +627,7 @@ constexpr int kXcds = 8;
 constexpr int kScanThreads = 512;
 
 template <bool kPrefetch>
-__global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
+__device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
   __shared__ float S[kD * 20];     // state slice (dk x 16), updated in place
   __shared__ float Vn0[kC * 20];   // new_values - k_cumdecay . S, first half of dk
   __shared__ float Vn1[kC * 20];   // k_cumdecay . S, second half of dk
@@ -786,6 +786,15 @@ __global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
     const int i = p / kW, j = p % kW;
     g.s_out[((int64_t)r * g.nv + h) * kD * kD + (int64_t)i * kD + col0 + j] = S[i * 20 + j];
   }
+}
+
+// Many chunks: the prefetching loop (up to 256 VGPRs, one workgroup per CU).
+__global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) { gdn_scan<true>(g); }
+// One chunk per (row, head): no loop to prefetch across, so the registers
+// are held to 128 and two workgroups share a CU, one loading while the
+// other computes.
+__global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(4))) void gdn_scan_one_chunk_kernel(GdnArgs g) {
+  gdn_scan<false>(g);
 }
 
 // ---------------------------------------------------------------------------
@@ -996,9 +1005,9 @@ extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, con
     hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3((unsigned)recs), dim3(kPrepThreads), 0, s, g);
   }
   if (g.n_chunks > 1)
-    hipLaunchKernelGGL(gdn_scan_kernel<true>, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
   else
-    hipLaunchKernelGGL(gdn_scan_kernel<false>, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
+    hipLaunchKernelGGL(gdn_scan_one_chunk_kernel, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
   // 16-byte aligned rows of z and y (and norm_w) for the vector norm
   const int64_t vec = d->dtype == CEV_BF16 ? 8 : 4;
   const bool norm_vec = ((uintptr_t)g.z | (uintptr_t)g.y | (uintptr_t)g.norm_w) % 16 == 0 && g.z_sb % vec == 0 && g.z_st % vec == 0 &&
