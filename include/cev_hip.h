@@ -247,6 +247,22 @@ int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, const void* x,
 int32_t cev_swiglu(int32_t dtype, int64_t rows, int32_t inter, const void* gate, const void* up, int64_t in_stride, void* out,
                    int64_t out_stride, cev_stream stream);
 
+/* Debiased readout scores: Service::run_debiased's averaging over rotated
+ * question variants (crates/cev-runtime/src/service.rs:330-345) with
+ * math::log_softmax in f64 (crates/cev-core/src/math.rs:14-18).  Question q
+ * owns variants span_begin[q] .. span_begin[q] + span_len[q] - 1 and
+ * n_options[q] options (1..min(ld, 64)); for each of its variants v in
+ * order and position p < n_options[q]:
+ *   scores[q][order[v][p]] += (log_softmax(logits[v])[p] - log_softmax(calib[v])[p]) / span_len[q]
+ * (the calib term is 0 when calib is NULL: no calibration twins), then the
+ * f64 sums are stored as f32.  logits, calib and order are (n_variants, ld)
+ * row-major, scores (n_questions, ld); all device memory.  A question whose
+ * span lies outside [0, n_variants), whose option count is out of range or
+ * whose order is not a permutation of its options gets NaN scores. */
+int32_t cev_debias_scores(int32_t n_questions, int32_t n_variants, const int32_t* span_begin, const int32_t* span_len,
+                          const int32_t* n_options, const float* logits, const float* calib, const int32_t* order, int32_t ld,
+                          float* scores, cev_stream stream);
+
 /* ------------------------------------------------------------------ */
 /* Table builders (host only). */
 

@@ -107,6 +107,57 @@ def softmax64(z) -> np.ndarray:
     return e / e.sum(axis=-1, keepdims=True)
 
 
+def log_softmax64(z) -> np.ndarray:
+    """math::log_softmax (crates/cev-core/src/math.rs:14-18): the f32 max as
+    f64, lse = m + ln(sum e^(z - m)) with the sum taken in position order
+    (the reference's iterator), z - lse in f64."""
+    z = np.asarray(z, np.float32)
+    m = np.float64(z.max())
+    e = np.exp(z.astype(np.float64) - m)
+    s = np.cumsum(e)[-1]  # sequential, left to right
+    return z.astype(np.float64) - (m + np.log(s))
+
+
+def rotation_shifts(k: int, max_permutations: int):
+    """Debias::shifts for Permute / Full (crates/cev-core/src/compile.rs:127-136):
+    at most max_permutations rotations of k options, evenly spread."""
+    if k < 2:
+        return [0]
+    n = min(k, max(max_permutations, 1))
+    out = []
+    for i in range(n):
+        s = i * k // n
+        if not out or out[-1] != s:
+            out.append(s)
+    return out
+
+
+def rotated_order(order, shift: int):
+    """CompiledQuestion::rotated (crates/cev-core/src/compile.rs:67-73): the
+    option shown at position j is order[(j + shift) % k]."""
+    k = len(order)
+    return [order[(j + shift) % k] for j in range(k)]
+
+
+def debias_scores(logits, order, span_begin, span_len, n_options, calib=None) -> np.ndarray:
+    """Service::run_debiased's averaging (crates/cev-runtime/src/service.rs:
+    330-345): score[order[v][p]] += (lp_v[p] - base_v[p]) / n over the
+    question's variants v in order, f64, stored as f32."""
+    logits = np.asarray(logits, np.float32)
+    q_n, ld = len(span_begin), logits.shape[1]
+    out = np.zeros((q_n, ld), np.float32)
+    for q in range(q_n):
+        k, b, n = int(n_options[q]), int(span_begin[q]), int(span_len[q])
+        score = np.zeros(k, np.float64)
+        for v in range(b, b + n):
+            lp = log_softmax64(logits[v, :k])
+            base = log_softmax64(calib[v, :k]) if calib is not None else np.zeros(k)
+            for pos in range(k):
+                score[int(order[v][pos])] += (lp[pos] - base[pos]) / n
+        out[q, :k] = score.astype(np.float32)
+    return out
+
+
 def run_config(w, weights=None):
     """The whole config-2 flow on the oracle: prefill the head, one packed
     pass (tail + questions), code-head probabilities.  Returns

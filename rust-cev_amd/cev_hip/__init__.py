@@ -352,6 +352,29 @@ def swiglu(gate, up, out=None, stream=None):
     return out
 
 
+def debias_scores(logits, order, span_begin, span_len, n_options, calib=None, stream=None):
+    """Debiased option scores on the device (Service::run_debiased's
+    averaging, service.rs:330-345; math::log_softmax in f64, math.rs:14-18).
+    logits / calib: (variants, ld) f32; order, span_begin, span_len,
+    n_options: int32 device tensors.  Returns (questions, ld) f32."""
+    torch = _torch()
+    n_var, ld = logits.shape
+    n_q = span_begin.shape[0]
+    for name, t, dt in (("logits", logits, torch.float32), ("order", order, torch.int32), ("span_begin", span_begin, torch.int32),
+                        ("span_len", span_len, torch.int32), ("n_options", n_options, torch.int32)) + \
+            ((("calib", calib, torch.float32),) if calib is not None else ()):
+        if t.dtype != dt or not t.is_contiguous():
+            raise CevError(-1, f"debias_scores: {name} must be contiguous {dt}")
+    if order.shape != logits.shape or (calib is not None and calib.shape != logits.shape):
+        raise CevError(-1, "debias_scores: order / calib must match logits' shape")
+    if span_len.shape[0] != n_q or n_options.shape[0] != n_q:
+        raise CevError(-1, "debias_scores: one span and option count per question")
+    scores = torch.empty((n_q, ld), dtype=torch.float32, device=logits.device)
+    check(lib().cev_debias_scores(n_q, n_var, _ptr(span_begin), _ptr(span_len), _ptr(n_options), _ptr(logits),
+                                  _ptr(calib) if calib is not None else None, _ptr(order), ld, _ptr(scores), _stream_ptr(stream)))
+    return scores
+
+
 @dataclass
 class DeviceInfo:
     name: str

@@ -103,6 +103,7 @@ SIGNATURES = {
     "cev_gdn_forward": (i32, [C.POINTER(GdnDesc), P, P, P, P, P, P, P, P, P, P, P, P, P, P, C.c_size_t, P]),
     "cev_rms_norm": (i32, [i32, i64, i32, P, i64, P, i64, P, i64, P, C.c_float, i32, P, i64, P]),
     "cev_swiglu": (i32, [i32, i64, i32, P, P, i64, P, i64, P]),
+    "cev_debias_scores": (i32, [i32, i32, P, P, P, P, P, P, i32, P, P]),
     "cev_table_from_plans": (i32, [i32, Pi32, Pi32, Pi32, i32, Pi32, Pi32, PBlock, i32, Pi32, Pi32, i32, Pi32, Pi32]),
     "cev_table_from_rows": (i32, [i32, i32, i32, i32, Pi32, PBlock, i32]),
     "cev_table_from_segment_ids": (i32, [C.POINTER(C.c_uint32), i32, i32, PBlock, i32, Pi32]),

@@ -222,6 +222,76 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+
+// ---------------------------------------------------------------------------
+// Debiased readout scores (Service::run_debiased's averaging,
+// crates/cev-runtime/src/service.rs:330-345, with math::log_softmax,
+// crates/cev-core/src/math.rs:14-18).  One wave per question; lane p holds
+// position p of a variant's logits (k <= 64 options).  log_softmax in f64:
+// m = the f32 max, lse = m + ln(sum_j e^(z_j - m)) summed in position order
+// like the reference's iterator, lp_p = z_p - lse.  Every variant adds
+// (lp_p - base_p) / n to the score of option order[p], variants in span
+// order; base is the calibration twin's log_softmax (0 without one).
+struct DebiasArgs {
+  const int32_t* span_begin;
+  const int32_t* span_len;
+  const int32_t* n_options;
+  const float* logits;
+  const float* calib;
+  const int32_t* order;
+  float* scores;
+  int32_t n_variants, ld;
+};
+
+__device__ __forceinline__ double readlane_f64(double x, int j) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, j), hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), j);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// log_softmax at this lane's position of a k-wide row (lanes >= k: unused)
+__device__ __forceinline__ double log_softmax_lane(float z, int k, int lane) {
+  float m = -INFINITY;
+  for (int j = 0; j < k; ++j) m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, z), j)));
+  const double m64 = (double)m;
+  const double e = lane < k ? exp((double)z - m64) : 0.0;
+  double sum = 0.0;
+  for (int j = 0; j < k; ++j) sum += readlane_f64(e, j);
+  return (double)z - (m64 + log(sum));
+}
+
+__global__ __launch_bounds__(64) void debias_kernel(DebiasArgs a) {
+  __shared__ double score[64];
+  const int q = blockIdx.x, lane = threadIdx.x;
+  score[lane] = 0.0;
+  const int k = a.n_options[q], b = a.span_begin[q], n = a.span_len[q];
+  float* out = a.scores + (int64_t)q * a.ld;
+  // a span outside the variants or an option count outside [1, min(ld, 64)]:
+  // the question's scores are NaN (a launch cannot return an error)
+  const bool span_ok = k >= 1 && k <= min(a.ld, 64) && n >= 1 && b >= 0 && b <= a.n_variants - n;
+  if (!span_ok) {
+    if (lane < a.ld) out[lane] = __builtin_nanf("");
+    return;
+  }
+  bool order_ok = true;
+  for (int v = b; v < b + n; ++v) {
+    const int64_t row = (int64_t)v * a.ld;
+    const float z = lane < k ? a.logits[row + lane] : 0.0f;
+    double d = log_softmax_lane(z, k, lane);
+    if (a.calib) d -= log_softmax_lane(lane < k ? a.calib[row + lane] : 0.0f, k, lane);
+    const int o = lane < k ? a.order[row + lane] : 0;
+    order_ok &= o >= 0 && o < k;
+    // order is a permutation: each option gets one lane's term per variant;
+    // the barrier keeps variants in order (LDS work of one wave)
+    if (lane < k && o >= 0 && o < k) score[o] += d / (double)n;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  const bool all_ok = __all(order_ok);
+  if (lane < k) out[lane] = all_ok ? (float)score[lane] : __builtin_nanf("");
+}
+
 }  // namespace
 
 extern "C" int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h,
@@ -276,5 +346,19 @@ extern "C" int32_t cev_swiglu(int32_t dtype, int64_t rows, int32_t inter, const 
     hipLaunchKernelGGL(swiglu_kernel<float>, dim3((unsigned)grid), dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "cev_swiglu launch: %s", hipGetErrorString(e));
+  return CEV_OK;
+}
+
+extern "C" int32_t cev_debias_scores(int32_t n_questions, int32_t n_variants, const int32_t* span_begin, const int32_t* span_len,
+                                     const int32_t* n_options, const float* logits, const float* calib, const int32_t* order, int32_t ld,
+                                     float* scores, cev_stream stream) {
+  CEV_CHECK_ARG(n_questions >= 0 && n_variants >= 0, "cev_debias_scores: negative count");
+  CEV_CHECK_ARG(ld >= 1 && ld <= 64, "cev_debias_scores: row width %d outside [1, 64]", ld);
+  if (n_questions == 0) return CEV_OK;
+  CEV_CHECK_ARG(span_begin && span_len && n_options && logits && order && scores, "cev_debias_scores: null buffer");
+  DebiasArgs a{span_begin, span_len, n_options, logits, calib, order, scores, n_variants, ld};
+  hipLaunchKernelGGL(debias_kernel, dim3((unsigned)n_questions), dim3(64), 0, (hipStream_t)stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "cev_debias_scores launch: %s", hipGetErrorString(e));
   return CEV_OK;
 }

@@ -487,3 +487,77 @@ def test_gdn_layer_value_heads_follow_key_heads_in_blocks(orc):
     assert np.abs(yp - want).max() < 1e-5
     # the tiled order (h % nk) would pair value head 1 with key head 1: not a symmetry of the layer
     assert np.abs(y.reshape(1, w.t, nv, dv)[:, :, 0] - y.reshape(1, w.t, nv, dv)[:, :, 2]).max() > 1e-3
+
+
+# ---------------------------------------------------------------- debiased readout
+
+
+def test_log_softmax64_closed_forms():
+    """math::log_softmax: constant logits give -ln k; it equals an
+    independent f64 log-softmax; shifting all logits by a constant (exactly
+    representable sums) changes nothing."""
+    from oracle.qwen3_stack import log_softmax64
+    for k in (1, 2, 5, 64):
+        assert np.allclose(log_softmax64(np.full(k, 3.25, np.float32)), -math.log(k), rtol=0, atol=1e-15)
+    z = RNG.standard_normal(37).astype(np.float32) * 4
+    zz = z.astype(np.float64)
+    ind = zz - zz.max() - np.log(np.exp(zz - zz.max()).sum())
+    assert np.allclose(log_softmax64(z), ind, rtol=0, atol=1e-13)
+    z = (np.round(RNG.standard_normal(37) * 4096) / 1024).astype(np.float32)  # z + 8 is exact in f32
+    assert np.allclose(log_softmax64(z), log_softmax64(z + np.float32(8.0)), rtol=0, atol=1e-12)
+
+
+def test_rotation_shifts_and_orders():
+    """Debias::shifts / CompiledQuestion::rotated by hand: 5 options, at most
+    4 rotations -> shifts 0, 1, 2, 3; 2 options -> 0, 1; 1 option -> 0."""
+    from oracle.qwen3_stack import rotated_order, rotation_shifts
+    assert rotation_shifts(5, 4) == [0, 1, 2, 3]
+    assert rotation_shifts(8, 4) == [0, 2, 4, 6]
+    assert rotation_shifts(2, 4) == [0, 1]
+    assert rotation_shifts(1, 4) == [0]
+    assert rotated_order([0, 1, 2, 3, 4], 2) == [2, 3, 4, 0, 1]
+
+
+def _invariant_case(rng, ks, max_perm=4):
+    """Variants of a position-invariant model (the reference's own check,
+    crates/cev-runtime/tests/runtime.rs:185-207): option o has the same logit
+    at every position it is shown in."""
+    from oracle.qwen3_stack import rotated_order, rotation_shifts
+    ld = max(ks)
+    rows, orders, begin, length, canon = [], [], [], [], []
+    for k in ks:
+        f = rng.standard_normal(k).astype(np.float32) * 2
+        canon.append(f)
+        begin.append(len(rows))
+        shifts = rotation_shifts(k, max_perm)
+        length.append(len(shifts))
+        for s in shifts:
+            order = rotated_order(list(range(k)), s)
+            row = np.zeros(ld, np.float32)
+            row[:k] = f[order]
+            rows.append(row)
+            orders.append(order + [0] * (ld - k))
+    return np.array(rows), np.array(orders, np.int32), np.array(begin), np.array(length), np.array(ks), canon
+
+
+def test_debias_rotations_map_back_to_canonical_options():
+    """Averaging the rotations of a position-invariant model reproduces the
+    undebiased log-probabilities per option (runtime.rs:185-207); an index
+    mix-up (scoring by position instead of option) breaks it."""
+    from oracle.qwen3_stack import debias_scores, log_softmax64
+    rng = np.random.default_rng(5)
+    logits, order, begin, length, ks, canon = _invariant_case(rng, [5, 2, 8, 3])
+    got = debias_scores(logits, order, begin, length, ks)
+    for q, k in enumerate(ks):
+        assert np.allclose(got[q, :k], log_softmax64(canon[q]), rtol=0, atol=1e-6)
+    wrong = debias_scores(logits, np.tile(np.arange(logits.shape[1], dtype=np.int32), (len(logits), 1)), begin, length, ks)
+    assert not np.allclose(wrong[0, :5], got[0, :5], rtol=0, atol=1e-3)
+
+
+def test_debias_calibration_against_itself_is_zero():
+    from oracle.qwen3_stack import debias_scores
+    rng = np.random.default_rng(6)
+    logits, order, begin, length, ks, _ = _invariant_case(rng, [4, 6])
+    logits = logits + rng.standard_normal(logits.shape).astype(np.float32)  # not invariant any more
+    got = debias_scores(logits, order, begin, length, ks, calib=logits)
+    assert np.array_equal(got, np.zeros_like(got))

@@ -159,3 +159,79 @@ def test_config2_full_f32_vs_golden(gpu):
     dh = float(np.abs(hid - g["hidden"]).max())
     _say(f"  |dp| {dp:.3g}  max|dhidden| {dh:.3g}")
     assert dp < P_TOL
+
+
+def _debias_inputs(rng, ks, max_perm=4, invariant=False):
+    from oracle.qwen3_stack import rotated_order, rotation_shifts
+    ld = max(ks)
+    rows, orders, begin, length = [], [], [], []
+    for k in ks:
+        f = rng.standard_normal(k).astype(np.float32) * 3
+        begin.append(len(rows))
+        shifts = rotation_shifts(k, max_perm)
+        length.append(len(shifts))
+        base = list(rng.permutation(k))
+        for s in shifts:
+            order = rotated_order(base, s)
+            row = rng.standard_normal(ld).astype(np.float32) * 3
+            if invariant:
+                row[:k] = f[order]
+            rows.append(row)
+            orders.append(order + [0] * (ld - k))
+    return (np.array(rows), np.array(orders, np.int32), np.array(begin, np.int32), np.array(length, np.int32),
+            np.array(ks, np.int32))
+
+
+def _device_debias(gpu, logits, order, begin, length, ks, calib=None):
+    import torch
+    import cev_hip
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)
+    out = cev_hip.debias_scores(t(logits), t(order), t(begin), t(length), t(ks), calib=None if calib is None else t(calib))
+    torch.cuda.synchronize()
+    return to_np(out)
+
+
+@pytest.mark.parametrize("calibrated", [False, True])
+def test_debias_scores_match_oracle(gpu, calibrated):
+    """cev_debias_scores against the oracle's restatement of
+    Service::run_debiased's averaging (service.rs:330-345): config 2's
+    16 questions x 4 rotations x 8 codes plus ragged option counts (1..64).
+    f64 exp / log may differ by an ulp between libm and the device: the f32
+    scores are held to 2 ulp-scale."""
+    from oracle.qwen3_stack import debias_scores
+    rng = np.random.default_rng(21 + calibrated)
+    ks = [8] * 16 + [2, 3, 5, 7, 1, 64, 13]
+    logits, order, begin, length, kk = _debias_inputs(rng, ks)
+    calib = rng.standard_normal(logits.shape).astype(np.float32) * 2 if calibrated else None
+    got = _device_debias(gpu, logits, order, begin, length, kk, calib)
+    want = debias_scores(logits, order, begin, length, kk, calib=calib)
+    for q, k in enumerate(ks):
+        d = np.abs(got[q, :k] - want[q, :k])
+        assert np.all(d <= 2.5e-7 * np.maximum(np.abs(want[q, :k]), 1.0)), (q, k, d.max())
+    _say(f"debias calibrated={calibrated}: {len(ks)} questions, max|d| {max(np.abs(got[q, :k] - want[q, :k]).max() for q, k in enumerate(ks)):.3g}")
+
+
+def test_debias_position_invariant_model_and_invalid_spans(gpu):
+    """The reference's own property (runtime.rs:185-207): averaging the
+    rotations of a position-invariant model gives each option its plain
+    log-probability.  Spans outside the variants, an option count of 0 and
+    an order that is not a permutation give NaN rows."""
+    from oracle.qwen3_stack import log_softmax64
+    rng = np.random.default_rng(9)
+    ks = [5, 2, 8]
+    logits, order, begin, length, kk = _debias_inputs(rng, ks, invariant=True)
+    got = _device_debias(gpu, logits, order, begin, length, kk)
+    for q, k in enumerate(ks):
+        # option o's logit is the same wherever it is shown: read it off variant 0
+        canon = np.empty(k, np.float32)
+        canon[order[begin[q], :k]] = logits[begin[q], :k]
+        assert np.allclose(got[q, :k], log_softmax64(canon), rtol=0, atol=2e-6)
+    bad_begin = np.array([0, len(logits) - 1, 0], np.int32)
+    bad_len = np.array([len(logits) + 1, 2, 1], np.int32)
+    bad_k = np.array([5, 2, 0], np.int32)
+    got = _device_debias(gpu, logits, order, bad_begin, bad_len, bad_k)
+    assert np.isnan(got).all()
+    broken = order.copy()
+    broken[begin[1], 0] = 2  # k = 2: option index out of range
+    got = _device_debias(gpu, logits, broken, begin, length, kk)
+    assert np.isnan(got[1, :2]).all() and np.isfinite(got[0, :5]).all() and np.isfinite(got[2, :8]).all()
