@@ -1,8 +1,8 @@
 """CPU oracle for cev's packed-prefill attention path (test infrastructure).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker (or as the timed
-CPU baseline).  The product path never calls it.
+``bench.py`` may import this package, and only to check results against (or as
+the timed CPU baseline).  The product path never calls it.
 
 The arithmetic lives in ``cev_oracle.c`` / ``gdn_oracle.c`` (built by the
 Makefile next to this file into ``oracle/build/liboracle.so``); this module is

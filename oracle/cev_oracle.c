@@ -2,8 +2,8 @@
  * CPU oracle for cev's packed-prefill attention path.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the
- * checker or as the timed CPU baseline -- never as the product path.
+ * cpu_baseline leg of bench.py may load this library, and only to check
+ * results against or as the timed CPU baseline -- never as the product path.
  *
  * What it restates (all paths relative to the reference checkout):
  *   - the RoPE cos/sin table        crates/cev-model/src/qwen3.rs:107-118,

@@ -1,7 +1,7 @@
 """The synthetic workloads of this path as concrete shapes and seeded inputs.
 
 Every tensor comes from cev_hip.synth with seed = workload number and its own
-stream id, so the GPU run and the CPU checker see identical values.  Arrays
+stream id, so the GPU run and the CPU oracle see identical values.  Arrays
 are f32 (holding bf16-exact values for bf16 workloads).
 
   c1  Qwen3-0.6B-shaped attention layer, f32: cached prefix P=256 (Hkv=8,

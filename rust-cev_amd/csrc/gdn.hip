@@ -101,7 +101,6 @@ struct GdnArgs {
 // Each product and partial sum is one model-dtype op (decoder.rs:143-150);
 // SiLU is candle's v / (1 + exp(-v)) with each op in the model dtype.
 constexpr int kConvRun = 16;
-constexpr int kConvMaxK = 8;
 
 template <typename T>
 __device__ __forceinline__ void load8(const T* p, float* v);
