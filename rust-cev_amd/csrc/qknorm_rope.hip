@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(la
   // y = dtype(dtype(x / m) * w) on chunk k, then rotate-half on the pairs
   // (i, i + ROT/2) of the first ROT elements; a position outside the table
   // yields NaN there instead of a stray read.
-  auto pair = [&](auto fast_c, u32x4& c0, u32x4& c1, int k) {
+  auto pair = [&](auto fast_c, u32x4& c0, u32x4& c1, int k, const u32x4& cc, const u32x4& sc) {
     constexpr bool FAST = decltype(fast_c)::value;
     auto quot = [&](float x) {
       if constexpr (FAST) {
@@ -291,8 +291,6 @@ __global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(la
         return x / m;
       }
     };
-    const u32x4 cc = *(const u32x4*)(crow + k * VEC);
-    const u32x4 sc = *(const u32x4*)(srow + k * VEC);
     float r0[VEC], r1[VEC];
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
@@ -331,11 +329,25 @@ __global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(la
   };
 
   if (__all(fast)) {
+    // the table chunks of pair k are loaded TPD pairs ahead, so their
+    // latency hides behind the pairs in between
+    constexpr int TPD = HC < 2 ? HC : 2;
+    u32x4 tcos[TPD > 0 ? TPD : 1], tsin[TPD > 0 ? TPD : 1];
+#pragma unroll
+    for (int k = 0; k < TPD; ++k) {
+      tcos[k] = *(const u32x4*)(crow + k * VEC);
+      tsin[k] = *(const u32x4*)(srow + k * VEC);
+    }
 #pragma unroll
     for (int k = 0; k < HC; ++k) {
-      pair(std::true_type{}, c[k], c[k + HC], k);
-      // keeps each chunk's weight and table reads next to their use
-      // (hoisted, they take a register each and cap the waves per SIMD)
+      const u32x4 cc = tcos[k % TPD], sc = tsin[k % TPD];
+      if (k + TPD < HC) {
+        tcos[k % TPD] = *(const u32x4*)(crow + (k + TPD) * VEC);
+        tsin[k % TPD] = *(const u32x4*)(srow + (k + TPD) * VEC);
+      }
+      pair(std::true_type{}, c[k], c[k + HC], k, cc, sc);
+      // keeps each chunk's weight reads and the table loads next to their
+      // use (hoisted, they take a register each and cap the waves per SIMD)
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -352,7 +364,7 @@ __global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(la
 #pragma unroll 1
     for (int k = 0; k < HC; ++k) {
       u32x4 c0 = *(const u32x4*)(src + k * VEC), c1 = *(const u32x4*)(src + (k + HC) * VEC);
-      pair(std::false_type{}, c0, c1, k);
+      pair(std::false_type{}, c0, c1, k, *(const u32x4*)(crow + k * VEC), *(const u32x4*)(srow + k * VEC));
       *(u32x4*)(dst + k * VEC) = c0;
       *(u32x4*)(dst + (k + HC) * VEC) = c1;
     }
