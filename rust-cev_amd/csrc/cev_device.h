@@ -27,6 +27,14 @@ __device__ __forceinline__ float swap_half(float x) { return __shfl_xor(x, 32, 6
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Orders this wave's LDS writes before its later LDS reads by other lanes of
+// the same wave (no workgroup barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <typename Fn, int... I>
 __device__ __forceinline__ void static_for_impl(Fn&& f, std::integer_sequence<int, I...>) {
   (f(std::integral_constant<int, I>{}), ...);

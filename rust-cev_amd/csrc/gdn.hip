@@ -246,12 +246,6 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 struct __attribute__((aligned(16))) PrepLds {
   float Qs[kC * kSX];  // q normalised * dk^-0.5; later k_cumdecay staging
   float Ks[kC * kSX];  // k normalised

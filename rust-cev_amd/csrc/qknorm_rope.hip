@@ -17,10 +17,12 @@
 // Two work splits, both summing each vector's squares in element order so
 // the sum matches the reference's sequential f32 sum bit for bit:
 //   qknorm_rope_lane_kernel (full rotary or a quarter of it, 16-byte aligned
-//     rows): one lane per vector (token, head).  The lane loads its vector
-//     in 16-byte chunks into registers, sums, normalises and rotates the
-//     pairs (i, i + rot/2) there and stores 16-byte chunks: no LDS, no
-//     barrier, one dependent add chain of D per lane.
+//     rows): one lane per vector (token, head).  A wave reads its 64 vectors
+//     with whole 128-byte lines and hands each lane its own vector through a
+//     per-wave LDS tile; the lane sums, normalises and rotates the pairs
+//     (i, i + rot/2) in registers, and the results go back out through the
+//     tile the same way: one dependent add chain of D per lane, no
+//     workgroup barrier after the weights.
 //   qknorm_rope_kernel (any other shape): a wave normalises 8 vectors at a
 //     time; lanes load coalesced, the squares go through LDS and lanes 0..7
 //     each sum one vector.
@@ -189,14 +191,26 @@ __device__ __forceinline__ void chunk_set2(u32x4& c, int i, float lo, float hi) 
 }
 
 constexpr int kLaneThreads = 256;
+constexpr int kStageRow = 144;      // bytes per vector row of a staging tile: 128 + 16 pad
+
+// A pointer into global memory (loads and stores through it are global, not
+// flat, instructions).
+template <typename V>
+using gptr = __attribute__((address_space(1))) V*;
+
+// The value of lane src's x (a 64-bit value in two permutes).
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t x, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)x, src, 64), hi = (uint32_t)__shfl((int)(uint32_t)(x >> 32), src, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
 
 // Waves per SIMD the register budget is held to: the packed vector takes
 // D * sizeof(T) / 16 * 4 registers per lane.
 template <typename T, int D>
 constexpr int lane_waves() { return D * (int)sizeof(T) >= 512 ? 3 : 4; }
 
-template <typename T, int D, int ROT>
-__global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(lane_waves<T, D>()))) void qknorm_rope_lane_kernel(
+template <typename T, int D, int ROT, int TPB>
+__global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<T, D>()))) void qknorm_rope_lane_kernel(
     QkArgs a) {
   constexpr bool BF = sizeof(T) == 2;
   constexpr int VEC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
@@ -208,7 +222,11 @@ __global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(la
   // The weights as the norm multiplies them (1 + w rounded to the dtype
   // for the zero-centred form), once per workgroup: q's then k's.
   __shared__ __align__(16) float weff[2][D];
-  for (int i = threadIdx.x; i < 2 * D; i += kLaneThreads) {
+  // per wave: 64 vectors x 128 bytes (one staging round) + 16 bytes of pad
+  constexpr int NR = NC / 8;  // staging rounds
+  static_assert(NC % 8 == 0, "whole staging rounds");
+  __shared__ __align__(16) char stage[TPB / 64][64 * kStageRow];
+  for (int i = threadIdx.x; i < 2 * D; i += TPB) {
     const T* wsrc = i < D ? (const T*)a.w_q : (const T*)a.w_k;
     const bool have = i < D ? a.hq > 0 : a.hkv > 0;
     float w = 0.0f;
@@ -225,28 +243,54 @@ __global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(la
 
   const int64_t nq = (int64_t)a.t * a.hq;
   const int64_t total = nq + (int64_t)a.t * a.hkv;
-  const int64_t v = (int64_t)blockIdx.x * kLaneThreads + threadIdx.x;
-  if (v >= total) return;
+  const int64_t v = (int64_t)blockIdx.x * TPB + threadIdx.x;
+  // Lanes past the last vector redo the last one, so that they take part in
+  // the staging exchange, and store nothing.
+  const bool valid = v < total;
+  const int64_t vv = valid ? v : total - 1;
   const T* src;
   T* dst;
   int tk;
-  const bool is_q = v < nq;
+  const bool is_q = vv < nq;
   if (is_q) {
-    tk = (int)(v / a.hq);
-    const int h = (int)(v % a.hq);
+    tk = (int)(vv / a.hq);
+    const int h = (int)(vv % a.hq);
     src = (const T*)a.q_in + tk * a.qi_st + h * a.qi_sh;
     dst = (T*)a.q_out + tk * a.qo_st + h * a.qo_sh;
   } else {
-    const int64_t vk = v - nq;
+    const int64_t vk = vv - nq;
     tk = (int)(vk / a.hkv);
     const int h = (int)(vk % a.hkv);
     src = (const T*)a.k_in + tk * a.ki_st + h * a.ki_sh;
     dst = (T*)a.k_out + tk * a.ko_st + h * a.ko_sh;
   }
   const float* wl = weff[is_q ? 0 : 1];
+  const int lane = threadIdx.x & 63;
+  char* st = stage[threadIdx.x >> 6];
   u32x4 c[NC];
+  {
+    // Staged load: in round q every instruction reads 128 bytes (chunks
+    // 8q .. 8q+7) of 8 vectors, lane l taking vector 8i + l/8, chunk l%8;
+    // the LDS tile then hands each lane its own vector.
+    const uint64_t sp = (uint64_t)src;
+    const int sub = lane >> 3, kc = lane & 7;
+    gptr<const u32x4> vp[8];
 #pragma unroll
-  for (int k = 0; k < NC; ++k) c[k] = *(const u32x4*)(src + k * VEC);
+    for (int i = 0; i < 8; ++i) vp[i] = (gptr<const u32x4>)shfl_u64(sp, 8 * i + sub) + kc;
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      u32x4 g[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) g[i] = vp[i][8 * q];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) *(u32x4*)(st + (8 * i + sub) * kStageRow + 16 * kc) = g[i];
+      wave_lds_sync();
+#pragma unroll
+      for (int k = 0; k < 8; ++k) c[8 * q + k] = *(const u32x4*)(st + lane * kStageRow + 16 * k);
+      wave_lds_sync();
+    }
+
+  }
   const int p = a.pos[tk];
 
   float sum2 = 0.0f;
@@ -355,9 +399,30 @@ __global__ __launch_bounds__(kLaneThreads) __attribute__((amdgpu_waves_per_eu(la
       single(std::true_type{}, c[k], k);
       __builtin_amdgcn_sched_barrier(0);
     }
+    // Staged store, the load's exchange in reverse: every instruction
+    // writes whole 128-byte lines.  The empty asm makes each pair pack its
+    // result where it is computed (sunk to the LDS writes, the unpacked
+    // values of every pair would stay live at once and spill).
 #pragma unroll
-    for (int k = 0; k < NC; ++k) *(u32x4*)(dst + k * VEC) = c[k];
-  } else {
+    for (int k = 0; k < NC; ++k) asm volatile("" : "+v"(c[k]));
+    const uint64_t dp = valid ? (uint64_t)dst : 0;
+    const int sub = lane >> 3, kc = lane & 7;
+    gptr<u32x4> vdst[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vdst[i] = (gptr<u32x4>)shfl_u64(dp, 8 * i + sub);
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) *(u32x4*)(st + lane * kStageRow + 16 * k) = c[8 * q + k];
+      wave_lds_sync();
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u32x4 val = *(const u32x4*)(st + (8 * i + sub) * kStageRow + 16 * kc);
+        if (vdst[i]) vdst[i][8 * q + kc] = val;
+      }
+      wave_lds_sync();
+    }
+  } else if (valid) {
     // Rare (a wave with a tiny, huge or non-finite element): IEEE division,
     // one chunk or rotary pair at a time, re-read from the input (each
     // chunk is read before its own store, so q_out may alias q_in).
@@ -394,27 +459,35 @@ bool lane_kernel_fits(const QkArgs& a, int d) {
   return a.rot == d || a.rot == d / 4;
 }
 
+template <typename T, int TPB>
+int32_t launch_lane(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
+  const int64_t grid = (vecs + TPB - 1) / TPB;
+  if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm grid too large");
+  const dim3 g((unsigned)grid), b(TPB);
+  if (d == 128 && a.rot == 128)
+    hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 128, 128, TPB>), g, b, 0, s, a);
+  else if (d == 128)
+    hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 128, 32, TPB>), g, b, 0, s, a);
+  else if constexpr (sizeof(T) == 2) {
+    if (a.rot == 256)
+      hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 256, 256, TPB>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 256, 64, TPB>), g, b, 0, s, a);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "qknorm_rope launch: %s", hipGetErrorString(e));
+  return CEV_OK;
+}
+
 template <typename T>
 int32_t launch_qk(const QkArgs& a, int d, hipStream_t s) {
   const int64_t vecs = (int64_t)a.t * (a.hq + a.hkv);
   if (vecs == 0) return CEV_OK;
   if (lane_kernel_fits<T>(a, d)) {
-    const int64_t grid = (vecs + kLaneThreads - 1) / kLaneThreads;
-    if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm grid too large");
-    const dim3 g((unsigned)grid), b(kLaneThreads);
-    if (d == 128 && a.rot == 128)
-      hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 128, 128>), g, b, 0, s, a);
-    else if (d == 128)
-      hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 128, 32>), g, b, 0, s, a);
-    else if constexpr (sizeof(T) == 2) {
-      if (a.rot == 256)
-        hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 256, 256>), g, b, 0, s, a);
-      else
-        hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 256, 64>), g, b, 0, s, a);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "qknorm_rope launch: %s", hipGetErrorString(e));
-    return CEV_OK;
+    // One-wave workgroups for a short call (under 64 workgroups of 256
+    // lanes), which then spreads over more CUs.
+    if (vecs < (int64_t)kLaneThreads * 64) return launch_lane<T, 64>(a, d, vecs, s);
+    return launch_lane<T, kLaneThreads>(a, d, vecs, s);
   }
   const int64_t per_wg = (int64_t)WAVES * VPW;
   const int64_t grid = (vecs + per_wg - 1) / per_wg;
