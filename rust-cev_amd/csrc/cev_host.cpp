@@ -328,7 +328,7 @@ int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, P
   }
   // Split the key stream of every tile when that shortens the launch (few
   // long-prefix rows leave the GPU underfilled): each part still gets at
-  // least kSplitMinChunks key tiles.
+  // least kSplitMinChunks (f32: kSplitMinChunksF32) key tiles.
   int32_t max_chunks = 0;
   for (int32_t ti = 0; ti < p.n_tiles; ++ti) max_chunks = std::max(max_chunks, p.tiles[(size_t)ti * 8 + 4]);
   const int64_t items = (int64_t)p.n_tiles * d->n_kv_heads;
@@ -338,7 +338,8 @@ int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, P
     // kSplitTargetWorkgroups workgroups, whichever has the smaller modelled
     // time: rounds x the longest part's chunks, plus the merge pass when
     // split; on a tie the larger part count (a fuller round).
-    int64_t cap = std::min<int64_t>(std::max(1, max_chunks / kSplitMinChunks), kSplitMax);
+    const int min_chunks = d->dtype == CEV_F32 ? kSplitMinChunksF32 : kSplitMinChunks;
+    int64_t cap = std::min<int64_t>(std::max(1, max_chunks / min_chunks), kSplitMax);
     if (d->max_splits > 1) cap = std::min<int64_t>(cap, d->max_splits);
     cap = std::min<int64_t>(cap, std::max<int64_t>(1, kSplitTargetWorkgroups / items));
     int64_t best = -1;

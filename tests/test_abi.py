@@ -291,6 +291,13 @@ def test_split_policy(cev):
     tab = cev_hip.BlockTable.from_rows(32, 64, 4096, causal=True)
     d = cev_hip.attn_desc(CEV_BF16, 16, 4, 256, tab.t, tab.s_cache, has_gate=True)
     assert cev_hip.AttnPlan(d, tab).n_splits == 2
+    # f32 chunks are long: 24 items of 12 chunks (12 x 32-token blocks after a
+    # 256-token prefix) take parts of 2 chunks; bf16 parts stay >= 4 chunks
+    tab = cev_hip.BlockTable.from_rows(12, 32, 256, causal=True)
+    d = cev_hip.attn_desc(CEV_F32, 16, 8, 128, tab.t, tab.s_cache)
+    assert cev_hip.AttnPlan(d, tab).n_splits == 6
+    d = cev_hip.attn_desc(CEV_BF16, 16, 8, 128, tab.t, tab.s_cache)
+    assert cev_hip.AttnPlan(d, tab).n_splits == 1
 
 
 def test_launch_requires_workspace_for_split_plans(cev):
