@@ -48,6 +48,7 @@ enum { CEV_F32 = 0, CEV_BF16 = 1 };
 #define CEV_MAX_SPANS 4
 
 typedef void* cev_stream;
+typedef void* cev_event; /* a hipEvent_t */
 
 /* ------------------------------------------------------------------ */
 /* Block-offset table.
@@ -311,9 +312,18 @@ int32_t cev_malloc(void** ptr, size_t bytes);
 int32_t cev_free(void* ptr);
 int32_t cev_memcpy_h2d(void* dst, const void* src, size_t bytes, cev_stream stream);
 int32_t cev_memcpy_d2h(void* dst, const void* src, size_t bytes, cev_stream stream);
+int32_t cev_memcpy_d2d(void* dst, const void* src, size_t bytes, cev_stream stream);
 int32_t cev_stream_create(cev_stream* stream);
 int32_t cev_stream_destroy(cev_stream stream);
 int32_t cev_stream_synchronize(cev_stream stream);
+/* Kernel timing (the FFI crate's counterpart of the harness's event timers):
+ * record `start` and `end` on the stream around the launches, synchronize
+ * on `end`, then read the milliseconds between the two. */
+int32_t cev_event_create(cev_event* event);
+int32_t cev_event_destroy(cev_event event);
+int32_t cev_event_record(cev_event event, cev_stream stream);
+int32_t cev_event_synchronize(cev_event event);
+int32_t cev_event_elapsed_ms(cev_event start, cev_event end, float* ms);
 
 #ifdef __cplusplus
 }

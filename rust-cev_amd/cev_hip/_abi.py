@@ -119,6 +119,12 @@ SIGNATURES = {
     "cev_stream_create": (i32, [C.POINTER(P)]),
     "cev_stream_destroy": (i32, [P]),
     "cev_stream_synchronize": (i32, [P]),
+    "cev_memcpy_d2d": (i32, [P, P, C.c_size_t, P]),
+    "cev_event_create": (i32, [C.POINTER(P)]),
+    "cev_event_destroy": (i32, [P]),
+    "cev_event_record": (i32, [P, P]),
+    "cev_event_synchronize": (i32, [P]),
+    "cev_event_elapsed_ms": (i32, [P, P, C.POINTER(C.c_float)]),
 }
 
 _lib = None

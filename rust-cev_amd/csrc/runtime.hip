@@ -42,6 +42,10 @@ extern "C" int32_t cev_memcpy_d2h(void* dst, const void* src, size_t bytes, cev_
   return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream), "hipMemcpyAsync d2h");
 }
 
+extern "C" int32_t cev_memcpy_d2d(void* dst, const void* src, size_t bytes, cev_stream stream) {
+  return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "hipMemcpyAsync d2d");
+}
+
 extern "C" int32_t cev_stream_create(cev_stream* stream) {
   CEV_CHECK_ARG(stream != nullptr, "cev_stream_create: null output");
   hipStream_t s;
@@ -55,4 +59,32 @@ extern "C" int32_t cev_stream_destroy(cev_stream stream) { return hip_status(hip
 
 extern "C" int32_t cev_stream_synchronize(cev_stream stream) {
   return hip_status(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+// Timing events: record two on a stream around the launches to time, wait
+// for the second, then read the milliseconds between them.
+extern "C" int32_t cev_event_create(cev_event* event) {
+  CEV_CHECK_ARG(event != nullptr, "cev_event_create: null output");
+  hipEvent_t e;
+  int32_t rc = hip_status(hipEventCreate(&e), "hipEventCreate");
+  if (rc) return rc;
+  *event = (cev_event)e;
+  return CEV_OK;
+}
+
+extern "C" int32_t cev_event_destroy(cev_event event) { return hip_status(hipEventDestroy((hipEvent_t)event), "hipEventDestroy"); }
+
+extern "C" int32_t cev_event_record(cev_event event, cev_stream stream) {
+  CEV_CHECK_ARG(event != nullptr, "cev_event_record: null event");
+  return hip_status(hipEventRecord((hipEvent_t)event, (hipStream_t)stream), "hipEventRecord");
+}
+
+extern "C" int32_t cev_event_synchronize(cev_event event) {
+  CEV_CHECK_ARG(event != nullptr, "cev_event_synchronize: null event");
+  return hip_status(hipEventSynchronize((hipEvent_t)event), "hipEventSynchronize");
+}
+
+extern "C" int32_t cev_event_elapsed_ms(cev_event start, cev_event end, float* ms) {
+  CEV_CHECK_ARG(start != nullptr && end != nullptr && ms != nullptr, "cev_event_elapsed_ms: null argument");
+  return hip_status(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end), "hipEventElapsedTime");
 }

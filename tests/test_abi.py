@@ -311,3 +311,13 @@ def test_launch_requires_workspace_for_split_plans(cev):
     L = _abi.lib()
     assert L.cev_packed_attention(C.byref(d), hp, fake, fake, fake, fake, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
     assert L.cev_packed_attention(C.byref(d), hp, fake, fake, fake, fake, fake, fake, None, fake, fake, 16, None) == CEV_ERR_SPACE
+
+
+def test_runtime_helpers_validate_before_any_gpu_call(cev):
+    L = _abi.lib()
+    assert L.cev_event_create(None) == CEV_ERR_INVALID
+    assert L.cev_event_record(None, None) == CEV_ERR_INVALID
+    assert L.cev_event_synchronize(None) == CEV_ERR_INVALID
+    assert L.cev_event_elapsed_ms(None, None, None) == CEV_ERR_INVALID
+    assert L.cev_malloc(None, 16) == CEV_ERR_INVALID
+    assert L.cev_stream_create(None) == CEV_ERR_INVALID
