@@ -27,6 +27,17 @@ __device__ __forceinline__ float swap_half(float x) { return __shfl_xor(x, 32, 6
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A value moved across lanes by a DPP control (row-local permutes such as
+// quad_perm 0x4E = lane ^ 2); every lane of the row must be active.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kCtrl, 0xF, 0xF, false);
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __uint_as_float(dpp_u<kCtrl>(__float_as_uint(v)));
+}
+
 // Orders this wave's LDS writes before its later LDS reads by other lanes of
 // the same wave (no workgroup barrier).
 __device__ __forceinline__ void wave_lds_sync() {

@@ -231,11 +231,6 @@ constexpr int kPrepThreads = 512;
 constexpr int kPrepWaves = kPrepThreads / 64;
 static_assert(kPrepWaves == 8, "the prep kernel's work split assumes 8 waves");
 
-template <int kCtrl>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
-}
-
 // Sum over the 16 lanes of a DPP row.  Every lane ends with the same bits:
 // each step adds two values that the partner lane adds in the other order.
 __device__ __forceinline__ float row16_sum(float x) {

@@ -14,7 +14,7 @@
 // rounded HIP forms (hipcc's default); __fsqrt_rn is not (it maps to the
 // native approximate square root) and must not be used here.
 //
-// Two work splits, both summing each vector's squares in element order so
+// Three work splits, all summing each vector's squares in element order so
 // the sum matches the reference's sequential f32 sum bit for bit:
 //   qknorm_rope_lane_kernel (full rotary or a quarter of it, 16-byte aligned
 //     rows): one lane per vector (token, head).  A wave reads its 64 vectors
@@ -23,6 +23,8 @@
 //     (i, i + rot/2) in registers, and the results go back out through the
 //     tile the same way: one dependent add chain of D per lane, no
 //     workgroup barrier after the weights.
+//   qknorm_rope_quad_kernel (the same shapes, calls under 16,384 vectors):
+//     four lanes per vector, the sum handed from lane to lane in order.
 //   qknorm_rope_kernel (any other shape): a wave normalises 8 vectors at a
 //     time; lanes load coalesced, the squares go through LDS and lanes 0..7
 //     each sum one vector.
@@ -459,6 +461,209 @@ bool lane_kernel_fits(const QkArgs& a, int d) {
   return a.rot == d || a.rot == d / 4;
 }
 
+// Calls with few vectors (a short suffix, small test passes) leave most
+// SIMDs idle under the one-lane-per-vector split, and one lane's ~2,000
+// dependent instructions then set the time.  Here a DPP quad (4 lanes)
+// holds one vector, a contiguous quarter per lane.  The sum of squares still
+// runs in element order: quad lane j adds its quarter to lane j-1's total.
+// The rotate-half partners of full rotary sit two lanes apart (quad_perm
+// lane ^ 2); a quarter rotary lies in lane 0's quarter.  Same per-element
+// ops and division as the lane kernel, so the results are the same bits.
+constexpr int kQuadThreads = 64;         // one wave: 16 vectors per workgroup
+constexpr int64_t kQuadMaxVecs = 16384;  // calls below this use the quad split
+
+template <typename T, int D, int ROT>
+__global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int VEC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  constexpr int E = D / 4;                  // elements per lane
+  constexpr int NCL = E / VEC;              // chunks per lane
+  static_assert(E % VEC == 0 && (ROT == D || ROT == D / 4), "whole chunks; full or quarter rotary");
+  auto rnd = [](float x) { return BF ? bf16_round(x) : x; };
+  __shared__ __align__(16) float weff[2][D];
+  for (int i = threadIdx.x; i < 2 * D; i += kQuadThreads) {
+    const T* wsrc = i < D ? (const T*)a.w_q : (const T*)a.w_k;
+    const bool have = i < D ? a.hq > 0 : a.hkv > 0;
+    float w = 0.0f;
+    if (have) {
+      if constexpr (BF)
+        w = bf16_from_bits(((const uint16_t*)wsrc)[i % D]);
+      else
+        w = ((const float*)wsrc)[i % D];
+      if (a.plus_one) w = rnd(w + 1.0f);
+    }
+    weff[i / D][i % D] = w;
+  }
+  __syncthreads();
+
+  const int64_t nq = (int64_t)a.t * a.hq;
+  const int64_t total = nq + (int64_t)a.t * a.hkv;
+  const int j = threadIdx.x & 3;
+  const int64_t v = ((int64_t)blockIdx.x * kQuadThreads + threadIdx.x) >> 2;
+  // Quads past the last vector redo the last one (every lane of a quad must
+  // take part in the DPP moves) and store nothing.
+  const bool valid = v < total;
+  const int64_t vv = valid ? v : total - 1;
+  const T* src;
+  T* dst;
+  int tk;
+  const bool is_q = vv < nq;
+  if (is_q) {
+    tk = (int)(vv / a.hq);
+    const int h = (int)(vv % a.hq);
+    src = (const T*)a.q_in + tk * a.qi_st + h * a.qi_sh;
+    dst = (T*)a.q_out + tk * a.qo_st + h * a.qo_sh;
+  } else {
+    const int64_t vk = vv - nq;
+    tk = (int)(vk / a.hkv);
+    const int h = (int)(vk % a.hkv);
+    src = (const T*)a.k_in + tk * a.ki_st + h * a.ki_sh;
+    dst = (T*)a.k_out + tk * a.ko_st + h * a.ko_sh;
+  }
+  const float* wl = weff[is_q ? 0 : 1] + j * E;
+  u32x4 c[NCL];
+#pragma unroll
+  for (int k = 0; k < NCL; ++k) c[k] = *(const u32x4*)(src + j * E + k * VEC);
+  const int p = a.pos[tk];
+
+  // smallest frexp exponent of a nonzero element over the quad (0 for 0)
+  int min_exp = 0;
+#pragma unroll
+  for (int k = 0; k < NCL; ++k)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) min_exp = min(min_exp, __builtin_amdgcn_frexp_expf(chunk_get<T>(c[k], e)));
+  min_exp = min(min_exp, (int)dpp_u<0xB1>((uint32_t)min_exp));  // lane ^ 1
+  min_exp = min(min_exp, (int)dpp_u<0x4E>((uint32_t)min_exp));  // lane ^ 2
+  // the sum of squares in element order, handed from lane to lane
+  float acc = 0.0f;
+#pragma unroll
+  for (int step = 0; step < 4; ++step) {
+    const float prev = dpp_f<0x90>(acc);  // quad_perm [0, 0, 1, 2]: lane j - 1's total
+    if (j == step) {
+      float s = step == 0 ? 0.0f : prev;
+#pragma unroll
+      for (int k = 0; k < NCL; ++k)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float x = chunk_get<T>(c[k], e);
+          s += x * x;
+        }
+      acc = s;
+    }
+  }
+  const float sum2 = dpp_f<0xFF>(acc);  // quad_perm [3, 3, 3, 3]: lane 3 holds the total
+  const float m = rnd(sqrtf(sum2 / (float)D + a.eps));
+  const bool fast = min_exp >= -95 && sum2 <= 0x1p120f && m >= 0x1p-20f && m <= 0x1p20f;
+  const float y = 1.0f / m;
+  const bool p_ok = p >= 0 && p < a.n_pos;
+  const T* crow = (const T*)a.cos_t + (int64_t)(p_ok ? p : 0) * (ROT / 2);
+  const T* srow = (const T*)a.sin_t + (int64_t)(p_ok ? p : 0) * (ROT / 2);
+
+  auto body = [&](auto fast_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    // dtype(dtype(x / m) * w) for element e of chunk k
+    auto norm = [&](const u32x4& ck, int k, int e) {
+      const float x = chunk_get<T>(ck, e);
+      float q;
+      if constexpr (FAST) {
+        const float q0 = x * y;
+        q = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, m, x), y, q0), q0);
+      } else {
+        q = x / m;
+      }
+      return rnd(rnd(q) * wl[k * VEC + e]);
+    };
+    if constexpr (ROT == D) {
+      // lane j < 2 holds x_i of the pair (x_i, x_{i + D/2}), lane j + 2 the
+      // other: r = dtype(ya * ca) + dtype(yb * cb) gives
+      //   x_i'         = dtype(x_i c) - dtype(x_{i+D/2} s)   (j < 2),
+      //   x_{i+D/2}'   = dtype(x_i s) + dtype(x_{i+D/2} c)   (j >= 2).
+      const bool first = j < 2;
+      const int ib = (j & 1) * E;  // table index of this lane's first element
+#pragma unroll
+      for (int k = 0; k < NCL; ++k) {
+        float yo[VEC], yp[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) yo[e] = norm(c[k], k, e);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) yp[e] = dpp_f<0x4E>(yo[e]);  // the partner's (lane ^ 2)
+        const u32x4 cc = *(const u32x4*)(crow + ib + k * VEC), sc = *(const u32x4*)(srow + ib + k * VEC);
+        float r[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float co = p_ok ? chunk_get<T>(cc, e) : __builtin_nanf("");
+          const float si = p_ok ? chunk_get<T>(sc, e) : __builtin_nanf("");
+          const float ya = first ? yo[e] : yp[e];
+          const float yb = first ? yp[e] : yo[e];
+          const float ca = first ? co : si, cb = first ? -si : co;
+          r[e] = rnd(ya * ca) + rnd(yb * cb);
+        }
+#pragma unroll
+        for (int i = 0; i < VEC / 2; ++i) chunk_set2<T>(c[k], i, r[2 * i], r[2 * i + 1]);
+      }
+    } else {
+      // quarter rotary: the pairs (i, i + E/2) of lane 0's quarter
+      constexpr int HC = NCL / 2;
+      if (j == 0) {
+#pragma unroll
+        for (int k = 0; k < HC; ++k) {
+          const u32x4 cc = *(const u32x4*)(crow + k * VEC), sc = *(const u32x4*)(srow + k * VEC);
+          float r0[VEC], r1[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float y0 = norm(c[k], k, e), y1 = norm(c[k + HC], k + HC, e);
+            const float co = p_ok ? chunk_get<T>(cc, e) : __builtin_nanf("");
+            const float si = p_ok ? chunk_get<T>(sc, e) : __builtin_nanf("");
+            r0[e] = rnd(y0 * co) - rnd(y1 * si);
+            r1[e] = rnd(y0 * si) + rnd(y1 * co);
+          }
+#pragma unroll
+          for (int i = 0; i < VEC / 2; ++i) {
+            chunk_set2<T>(c[k], i, r0[2 * i], r0[2 * i + 1]);
+            chunk_set2<T>(c[k + HC], i, r1[2 * i], r1[2 * i + 1]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < NCL; ++k) {
+          float r[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) r[e] = norm(c[k], k, e);
+#pragma unroll
+          for (int i = 0; i < VEC / 2; ++i) chunk_set2<T>(c[k], i, r[2 * i], r[2 * i + 1]);
+        }
+      }
+    }
+  };
+  if (__all(fast))
+    body(std::true_type{});
+  else
+    body(std::false_type{});
+  if (valid) {
+#pragma unroll
+    for (int k = 0; k < NCL; ++k) *(u32x4*)(dst + j * E + k * VEC) = c[k];
+  }
+}
+
+template <typename T>
+int32_t launch_quad(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
+  const int64_t grid = (4 * vecs + kQuadThreads - 1) / kQuadThreads;
+  const dim3 g((unsigned)grid), b(kQuadThreads);
+  if (d == 128 && a.rot == 128)
+    hipLaunchKernelGGL((qknorm_rope_quad_kernel<T, 128, 128>), g, b, 0, s, a);
+  else if (d == 128)
+    hipLaunchKernelGGL((qknorm_rope_quad_kernel<T, 128, 32>), g, b, 0, s, a);
+  else if constexpr (sizeof(T) == 2) {
+    if (a.rot == 256)
+      hipLaunchKernelGGL((qknorm_rope_quad_kernel<T, 256, 256>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((qknorm_rope_quad_kernel<T, 256, 64>), g, b, 0, s, a);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "qknorm_rope launch: %s", hipGetErrorString(e));
+  return CEV_OK;
+}
+
 template <typename T, int TPB>
 int32_t launch_lane(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
   const int64_t grid = (vecs + TPB - 1) / TPB;
@@ -484,6 +689,7 @@ int32_t launch_qk(const QkArgs& a, int d, hipStream_t s) {
   const int64_t vecs = (int64_t)a.t * (a.hq + a.hkv);
   if (vecs == 0) return CEV_OK;
   if (lane_kernel_fits<T>(a, d)) {
+    if (vecs < kQuadMaxVecs) return launch_quad<T>(a, d, vecs, s);
     // One-wave workgroups for a short call (under 64 workgroups of 256
     // lanes), which then spreads over more CUs.
     if (vecs < (int64_t)kLaneThreads * 64) return launch_lane<T, 64>(a, d, vecs, s);

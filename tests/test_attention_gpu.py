@@ -293,15 +293,19 @@ def _same_bits(a, b):
     return bool(np.all(nan | (a.view(np.uint32) == b.view(np.uint32))))
 
 
+@pytest.mark.parametrize("repeat", [1, 30], ids=["quad", "lane"])
 @pytest.mark.parametrize("bf16,d,rot,plus_one,inplace", [(True, 128, 128, False, False), (True, 256, 64, True, False),
-                                                         (False, 128, 128, False, False), (True, 128, 128, False, True)])
-def test_qknorm_rope_bit_exact_on_extreme_values(gpu, orc, bf16, d, rot, plus_one, inplace):
-    """One lane normalises one vector; a wave whose vectors are all in the
-    fast division's range divides by reciprocal + FMA correction, any other
-    wave uses IEEE division.  Vectors with zeros, -0, elements below 2^-96,
-    huge elements and ordinary ones (both kinds of waves, and waves that
-    mix them) must all match the oracle bit for bit, the sign of zero
-    included; the in-place form (q_out = q_in) too."""
+                                                         (False, 128, 128, False, False), (True, 128, 128, False, True),
+                                                         (True, 128, 32, False, False)])
+def test_qknorm_rope_bit_exact_on_extreme_values(gpu, orc, bf16, d, rot, plus_one, inplace, repeat):
+    """A call with few vectors gives each vector a DPP quad of lanes (576
+    vectors here); a larger one (the same tokens 30 times, 17,280 vectors)
+    gives each vector one lane.  A wave whose vectors are all in the fast
+    division's range divides by reciprocal + FMA correction, any other wave
+    uses IEEE division.  Vectors with zeros, -0, elements below 2^-96, huge
+    elements and ordinary ones (both kinds of waves, and waves that mix
+    them) must all match the oracle bit for bit, the sign of zero included;
+    the in-place form (q_out = q_in) too."""
     import torch
     from cev_hip import synth
     t, hq, hkv, eps, theta = 96, 4, 2, 1e-6, 1e6
@@ -327,6 +331,7 @@ def test_qknorm_rope_bit_exact_on_extreme_values(gpu, orc, bf16, d, rot, plus_on
     if bf16:
         wq, wk = synth.round_bf16(wq), synth.round_bf16(wk)
     pos = (np.arange(t) % 40 + 3).astype(np.int32)
+    q, k, pos = np.tile(q, (repeat, 1, 1)), np.tile(k, (repeat, 1, 1)), np.tile(pos, repeat)
     n_pos = 64
     rotary = cev_hip.Rotary(theta, rot, n_pos, dt, gpu)
     dq, dk = to_dev(q, bf16, gpu), to_dev(k, bf16, gpu)
