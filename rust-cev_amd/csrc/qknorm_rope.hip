@@ -658,6 +658,8 @@ int32_t launch_quad(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
       hipLaunchKernelGGL((qknorm_rope_quad_kernel<T, 256, 256>), g, b, 0, s, a);
     else
       hipLaunchKernelGGL((qknorm_rope_quad_kernel<T, 256, 64>), g, b, 0, s, a);
+  } else {
+    return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm_rope: no quad kernel for f32 at d = %d", d);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "qknorm_rope launch: %s", hipGetErrorString(e));
@@ -678,6 +680,8 @@ int32_t launch_lane(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
       hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 256, 256, TPB>), g, b, 0, s, a);
     else
       hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 256, 64, TPB>), g, b, 0, s, a);
+  } else {
+    return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm_rope: no lane kernel for f32 at d = %d", d);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "qknorm_rope launch: %s", hipGetErrorString(e));
