@@ -324,8 +324,14 @@ def bench_stack(args, w, dev):
     table, pos, gather = BlockTable.from_plans(plans, items)
     tokens = np.concatenate([state[w.head_tokens:], qs.reshape(-1)])
 
+    tail = w.state_tokens - w.head_tokens
+
     def step():
-        return stack.code_logits(stack.forward_packed(tokens, pos, table, gather), codes)
+        # The pass keeps its tail's K/V in the cache, as forward_packed does;
+        # the cache length is then reset so every step repeats the same pass.
+        logits = stack.code_logits(stack.forward_packed(tokens, pos, table, gather, keep_tokens=tail), codes)
+        stack.cached -= tail
+        return logits
 
     for _ in range(args.warmup):
         step()
