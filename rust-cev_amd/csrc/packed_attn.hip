@@ -443,6 +443,9 @@ __device__ __forceinline__ i32x4 read_b128(int vaddr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(vaddr), "i"(OFF) : "memory");
   return r;
 }
+// One K operand fragment: a 16-byte read per lane.  Two 8-byte reads of
+// the same bytes measured no faster; the reads are bound by LDS bytes.
+typedef i32x4 KFrag;
 // LDS returns in order: once at most N LGKM operations are outstanding,
 // every LDS read issued before the last N LDS reads has landed (an older
 // scalar load still in flight only makes the wait stricter).
@@ -457,38 +460,60 @@ __device__ __forceinline__ void wait_b128(i32x4& r) {
   asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
 }
 
-// Issue order of the LDS reads of one sub-tile body (8 QK units, 8 PV
-// units, KPF = VPF = 3): three K reads up front; QK unit u then issues K
-// read u+3 (u < 5) or V fragment u-5 (u >= 5, two reads); PV unit j issues
-// V fragment j+3 (j < 5).  Each count below is the number of reads issued
-// after the one a unit waits for, up to that unit's wait.
-constexpr int kIssuedA(int u) { return (u + 3 < 8 ? 1 : 0) + (u >= 5 ? 2 : 0); }
-constexpr int kIssuedB(int j) { return j + 3 < 8 ? 2 : 0; }
-constexpr int kBeforeA(int st) {  // reads issued before QK unit st waits
-  int t = 3;
-  for (int u = 0; u < st; ++u) t += kIssuedA(u);
-  return t;
+// Issue order of the LDS reads of one sub-tile body (NQK = 8 QK units, then
+// NPV = 8 PV units).  QK unit u waits for K read u, then issues K read
+// u + kKPF (if any) and, in its last kVPF units, the two reads of V fragment
+// u - (8 - kVPF).  PV unit j waits for V fragment j, then issues V fragment
+// j + kVPF (if any) and, in its last kKPF units, K read j - (8 - kKPF) of the
+// next body.  The wait of each unit is the number of LDS reads issued after
+// the one it needs; the count below replays one steady-state body.
+// Four or five K fragments ahead measured within 0.5 % of three.
+constexpr int kKPF = 3;  // K fragments in flight ahead of their MFMA
+constexpr int kVPF = 3;  // V fragments in flight ahead of their MFMA
+static_assert(kKPF >= 1 && kKPF <= 8 && kVPF >= 1 && kVPF <= 8, "prefetch depths");
+struct ReadSchedule {
+  int wait_a[8], wait_b[8];
+};
+constexpr ReadSchedule read_schedule() {
+  ReadSchedule r{};
+  int kpos[8] = {}, vhi[8] = {};
+  int pos = 0;
+  // the previous body's PV units: V reads of that body, then this body's
+  // first kKPF K reads
+  for (int j = 0; j < 8; ++j) {
+    if (j + kVPF < 8) pos += 2;
+    if (j >= 8 - kKPF) kpos[j - (8 - kKPF)] = pos++;
+  }
+  for (int u = 0; u < 8; ++u) {
+    r.wait_a[u] = pos - kpos[u] - 1;
+    if (u + kKPF < 8) kpos[u + kKPF] = pos++;
+    if (u >= 8 - kVPF) {
+      vhi[u - (8 - kVPF)] = pos + 1;
+      pos += 2;
+    }
+  }
+  for (int j = 0; j < 8; ++j) {
+    r.wait_b[j] = pos - vhi[j] - 1;
+    if (j + kVPF < 8) {
+      vhi[j + kVPF] = pos + 1;
+      pos += 2;
+    }
+    if (j >= 8 - kKPF) ++pos;
+  }
+  return r;
 }
-constexpr int kPosK(int st) {  // issue position of K read st
-  if (st < 3) return st;
-  int t = 3;
-  for (int u = 0; u < st - 3; ++u) t += kIssuedA(u);
-  return t;
+constexpr ReadSchedule kReads = read_schedule();
+constexpr int kWaitA(int st) { return kReads.wait_a[st]; }
+constexpr int kWaitB(int j) { return kReads.wait_b[j]; }
+constexpr bool waits_in_range() {
+  for (int i = 0; i < 8; ++i)
+    if (kReads.wait_a[i] < 0 || kReads.wait_a[i] > 15 || kReads.wait_b[i] < 0 || kReads.wait_b[i] > 15) return false;
+  return true;
 }
-constexpr int kWaitA(int st) { return kBeforeA(st) - kPosK(st) - 1; }
-constexpr int kPosVhi(int j) {  // issue position of the second read of V fragment j
-  if (j < 3) return kBeforeA(5 + j) + 1;
-  int t = kBeforeA(8);
-  for (int b = 0; b < j - 3; ++b) t += kIssuedB(b);
-  return t + 1;
-}
-constexpr int kWaitB(int j) {
-  int t = kBeforeA(8);
-  for (int b = 0; b < j; ++b) t += kIssuedB(b);
-  return t - kPosVhi(j) - 1;
-}
-static_assert(kWaitA(0) == 2 && kWaitA(5) == 2 && kWaitA(6) == 3 && kWaitA(7) == 4, "QK wait counts");
-static_assert(kWaitB(0) == 4 && kWaitB(5) == 4 && kWaitB(6) == 2 && kWaitB(7) == 0, "PV wait counts");
+static_assert(waits_in_range(), "lgkmcnt range");
+static_assert((kWaitA(0) == 2 && kWaitA(5) == 2 && kWaitA(6) == 3 && kWaitA(7) == 4 && kWaitB(0) == 4 &&
+                   kWaitB(4) == 4 && kWaitB(5) == 4 && kWaitB(6) == 3 && kWaitB(7) == 2),
+              "wait counts at three fragments ahead");
 }  // namespace pipe
 
 template <typename T, int D>
@@ -586,7 +611,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
       constexpr int OFF = decltype(buf_c)::value * kTileBytes + decltype(kt_c)::value * 32 * kRowBytes;
       return read_b128<OFF>(lds_base + koff[decltype(st_c)::value]);
     };
-    auto k_ready = [](i32x4& r, auto st_c) {
+    auto k_ready = [](KFrag& r, auto st_c) {
       wait_b128<kWaitA(decltype(st_c)::value)>(r);
       return __builtin_bit_cast(bf16x8, r);
     };
@@ -670,6 +695,18 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sa[i]);
       }
     }
+    // K reads in flight into the next body: the first body's are issued
+    // here (sub-tile 1 of chunk 0) and waited for in full, so that its
+    // counted waits see no fewer reads than a steady-state body's.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    KFrag kf[kKPF];
+    if (wave_active) {
+      static_for<kKPF>([&](auto f_c) { kf[decltype(f_c)::value] = k_issue(I0{}, I1{}, f_c); });
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
 
     // ---- main loop, software-pipelined over 32-key sub-tiles j:
     //   scores S(j+1) = K(j+1) . Q^T run on the MFMA unit while the VALU
@@ -707,22 +744,18 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
           }
           const float mc = -m_run;
           float rs = 0.0f, m2 = -INFINITY;
-          constexpr int KPF = 3;  // K fragments in flight ahead of their MFMA
-          constexpr int VPF = 3;  // V fragments in flight ahead of their MFMA
+          constexpr int KPF = kKPF, VPF = kVPF;
           // Each unit below ends in a scheduling fence, so the order is the
           // program order unit by unit: one MFMA of one stream next to the
           // VALU work of the other, with operand reads KPF / VPF units ahead
           // of their MFMA.  The part's last sub-tile also scores a "next"
           // one from a buffer of stale or zero keys, never used: that keeps
           // O out of a branch (where the compiler copies all 64 accumulators).
-          static_assert(KPF == 3 && VPF == 3, "the wait counts assume three fragments ahead");
           using BN_c = std::integral_constant<int, bn>;
           using KTN_c = std::integral_constant<int, ktn>;
-          i32x4 kf[KPF];
           VFrag vf[VPF];
           P p;
           sn = f32x16{};
-          static_for<KPF>([&](auto f_c) { kf[decltype(f_c)::value] = k_issue(BN_c{}, KTN_c{}, f_c); });
           const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
           // Region A: QK(j+1) on the MFMA unit; exp(j), P(j) and its row sum
           // on the VALU, two probabilities per unit.  Its last VPF units
@@ -748,6 +781,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
             F::pv_mfma(v_ready(vf[j % VPF], j_c), j, p, o);
             if constexpr (j + VPF < F::NPV)
               vf[j % VPF] = v_issue(std::integral_constant<int, B0>{}, kt_c, std::integral_constant<int, j + VPF>{});
+            // the next body's first K reads: it scores sub-tile kt + 2
+            if constexpr (j >= F::NPV - KPF)
+              kf[j - (F::NPV - KPF)] = k_issue(std::integral_constant<int, (B0 + (kt + 2) / 2) % kBuf>{},
+                                               std::integral_constant<int, (kt + 2) % 2>{},
+                                               std::integral_constant<int, j - (F::NPV - KPF)>{});
             m2 = fmaxf(m2, fmaxf(sn[2 * j], sn[2 * j + 1]));
             pin(m2);
             __builtin_amdgcn_sched_barrier(0);
@@ -767,10 +805,6 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
       for (int k = 0; k < kAhead; ++k) chs[k] = chs[k + 1];
     };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
     static_assert(kBuf == 4, "the unrolled loop below walks four buffers");
     for (int ci = 0; ci < nc; ci += kBuf) {
       step(ci, I0{});
@@ -782,8 +816,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
       step(ci + 3, I3{});
     }
     // Fetches past the part's end read no memory, but they still write
-    // zeros into LDS: drain them before the workgroup exits.
+    // zeros into LDS: drain them, and the last body's K reads of a sub-tile
+    // past the end, before the workgroup exits.
     wait_vmcnt<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 
   const float l = pair_sum(l_run);
