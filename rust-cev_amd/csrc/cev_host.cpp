@@ -135,7 +135,9 @@ struct Ival {
   int32_t b, e;  // [b, e)
 };
 
-int32_t check_desc(const cev_attn_desc* d) {
+}  // namespace
+
+int32_t cev_check_attn_desc(const cev_attn_desc* d) {
   CEV_CHECK_ARG(d != nullptr, "null attention descriptor");
   if (d->dtype != CEV_F32 && d->dtype != CEV_BF16) return cev_fail(CEV_ERR_UNSUPPORTED, "dtype %d not supported", d->dtype);
   if (d->head_dim != 128 && d->head_dim != 256) return cev_fail(CEV_ERR_UNSUPPORTED, "head_dim %d not supported (128, 256)", d->head_dim);
@@ -175,35 +177,41 @@ int32_t check_desc(const cev_attn_desc* d) {
   return CEV_OK;
 }
 
-bool overlaps(Ival a, Ival b) { return a.b < b.e && b.b < a.e; }
+namespace {
 
 int32_t check_blocks(const cev_attn_desc* d, const cev_block* blocks, int32_t n) {
   CEV_CHECK_ARG(n >= 0, "negative block count %d", n);
   CEV_CHECK_ARG(n == 0 || blocks != nullptr, "null block table");
   const int64_t keys = (int64_t)d->s_cache + d->t;
+  // Interval ends in int64: a begin near INT32_MAX plus a length must not
+  // wrap to a small end that passes the range checks.
+  struct Iv64 {
+    int64_t b, e;
+  };
+  auto ov = [](Iv64 x, Iv64 y) { return x.b < y.e && y.b < x.e; };
   for (int32_t i = 0; i < n; ++i) {
     const cev_block& b = blocks[i];
     CEV_CHECK_ARG(b.q_len >= 1, "block %d: q_len %d < 1", i, b.q_len);
-    CEV_CHECK_ARG(b.q_begin >= 0 && (int64_t)b.q_begin + b.q_len <= d->t, "block %d: rows [%d, %d) outside [0, %d)", i, b.q_begin,
-                  b.q_begin + b.q_len, d->t);
+    CEV_CHECK_ARG(b.q_begin >= 0 && (int64_t)b.q_begin + b.q_len <= d->t, "block %d: rows [%d, %lld) outside [0, %d)", i, b.q_begin,
+                  (long long)b.q_begin + b.q_len, d->t);
     CEV_CHECK_ARG(b.causal == 0 || b.causal == 1, "block %d: causal must be 0 or 1", i);
     if (b.causal)
       CEV_CHECK_ARG(b.valid_len == b.q_len, "block %d: a causal block has valid_len == q_len", i);
     else
       CEV_CHECK_ARG(b.valid_len >= 0 && b.valid_len <= b.q_len, "block %d: valid_len %d outside [0, %d]", i, b.valid_len, b.q_len);
     CEV_CHECK_ARG(b.n_spans >= 0 && b.n_spans <= CEV_MAX_SPANS, "block %d: n_spans %d outside [0, %d]", i, b.n_spans, CEV_MAX_SPANS);
-    Ival local{b.local_begin, b.local_begin + b.q_len};
-    CEV_CHECK_ARG(b.local_begin >= 0 && (int64_t)local.e <= keys, "block %d: local keys [%d, %d) outside [0, %lld)", i, local.b, local.e,
-                  (long long)keys);
+    const Iv64 local{b.local_begin, (int64_t)b.local_begin + b.q_len};
+    CEV_CHECK_ARG(b.local_begin >= 0 && local.e <= keys, "block %d: local keys [%d, %lld) outside [0, %lld)", i, b.local_begin,
+                  (long long)local.e, (long long)keys);
     for (int s = 0; s < b.n_spans; ++s) {
-      Ival sp{b.spans[s].begin, b.spans[s].begin + b.spans[s].len};
-      CEV_CHECK_ARG(b.spans[s].len >= 0 && sp.b >= 0 && (int64_t)sp.e <= keys, "block %d span %d: keys [%d, %d) outside [0, %lld)", i, s,
-                    sp.b, sp.e, (long long)keys);
+      const Iv64 sp{b.spans[s].begin, (int64_t)b.spans[s].begin + b.spans[s].len};
+      CEV_CHECK_ARG(b.spans[s].len >= 0 && sp.b >= 0 && sp.e <= keys, "block %d span %d: keys [%lld, %lld) outside [0, %lld)", i, s,
+                    (long long)sp.b, (long long)sp.e, (long long)keys);
       if (b.spans[s].len == 0) continue;
-      CEV_CHECK_ARG(!overlaps(sp, local), "block %d span %d overlaps the block's own keys", i, s);
+      CEV_CHECK_ARG(!ov(sp, local), "block %d span %d overlaps the block's own keys", i, s);
       for (int s2 = 0; s2 < s; ++s2) {
-        Ival o{b.spans[s2].begin, b.spans[s2].begin + b.spans[s2].len};
-        CEV_CHECK_ARG(!overlaps(sp, o), "block %d: spans %d and %d overlap", i, s2, s);
+        const Iv64 o{b.spans[s2].begin, (int64_t)b.spans[s2].begin + b.spans[s2].len};
+        CEV_CHECK_ARG(!ov(sp, o), "block %d: spans %d and %d overlap", i, s2, s);
       }
     }
   }
@@ -239,7 +247,7 @@ void push_seg(Plan& p, int32_t b, int32_t e, int32_t masked, int32_t s_cache) {
 constexpr int32_t kMinFullLocal = 128;
 
 int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, Plan& p) {
-  int32_t rc = check_desc(d);
+  int32_t rc = cev_check_attn_desc(d);
   if (rc) return rc;
   rc = check_blocks(d, blocks, n);
   if (rc) return rc;
@@ -402,6 +410,7 @@ extern "C" int32_t cev_attn_plan_build(const cev_attn_desc* d, const cev_block* 
   if (!p.tiles.empty()) memcpy(out + h.tiles_off, p.tiles.data(), 4 * p.tiles.size());
   if (!p.segs.empty()) memcpy(out + h.segs_off, p.segs.data(), 4 * p.segs.size());
   if (!p.rows.empty()) memcpy(out + h.rows_off, p.rows.data(), 4 * p.rows.size());
+  out[kPlanSigWord] = (int32_t)cev_plan_signature(out, (int32_t)(need / 4), kPlanSigWord);
   return CEV_OK;
 }
 

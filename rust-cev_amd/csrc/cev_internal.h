@@ -14,3 +14,7 @@ void cev_clear_error();
   do {                                                \
     if (!(cond)) return cev_fail(CEV_ERR_INVALID, __VA_ARGS__); \
   } while (0)
+
+// Validates an attention descriptor (dtype, shapes, strides, scale); the
+// planner runs it on every plan build and the launcher on every launch.
+int32_t cev_check_attn_desc(const cev_attn_desc* d);

@@ -24,16 +24,33 @@
 #endif
 
 #define CEV_PLAN_MAGIC 0x50564543  // "CEVP"
-#define CEV_PLAN_VERSION 2
+#define CEV_PLAN_VERSION 3
+
+// Signature of a plan blob: FNV-1a over its int32 words with the `sig`
+// word itself taken as zero.  The launcher passes the host plan's
+// signature to the kernels, which compare it with the device copy's.
+CEV_HD static inline uint32_t cev_plan_signature(const int32_t* words, int32_t n_words, int32_t sig_index) {
+  uint32_t h = 2166136261u;
+  for (int32_t i = 0; i < n_words; ++i) {
+    const uint32_t w = i == sig_index ? 0u : (uint32_t)words[i];
+    for (int b = 0; b < 4; ++b) {
+      h ^= (w >> (8 * b)) & 0xffu;
+      h *= 16777619u;
+    }
+  }
+  return h;
+}
 
 struct cev_plan_header {
   int32_t magic, version, n_tiles, n_segs;
   int32_t t, s_cache, tile_rows, dtype;
   int32_t head_dim, n_q_heads, n_kv_heads, tiles_off;  // offsets in int32 units
   int32_t segs_off, rows_off, bytes, n_splits;
-  int32_t block_n, reserved[3];
+  int32_t block_n, sig, reserved[2];
 };
 static_assert(sizeof(cev_plan_header) == 80, "plan header is 80 bytes");
+constexpr int32_t kPlanSigWord = 17;  // index of `sig` among the plan's int32 words
+static_assert(__builtin_offsetof(cev_plan_header, sig) == 4 * kPlanSigWord, "sig word index");
 
 // Waves per workgroup and query rows per tile for a GQA group size g:
 // every wave owns 32 rows of one query head, the 8 waves of a workgroup

@@ -44,15 +44,33 @@ struct AttnArgs {
   int64_t q_st, q_sh, kc_ss, kc_sh, vc_ss, vc_sh, kn_st, kn_sh, vn_st, vn_sh, g_st, g_sh, o_st, o_sh;
   int32_t n_tiles, t, s_cache, hq, hkv, g, has_gate, n_splits, tile_rows;
   float scale_log2;
+  uint32_t plan_sig;  // signature of the host plan this launch was validated with
 };
 
 constexpr float kRescale = 8.0f;
 
-// The plan header on the device must describe the launch; anything else
-// (a plan not copied from the host plan) makes every workgroup exit.
+// The plan header on the device must be the host plan's (same signature,
+// same launch shape).  A device plan that is not a copy of the validated
+// host plan is never followed: the attention kernels fill the whole output
+// with NaN instead (poison_output) and the merge pass writes nothing, so a
+// stale device plan shows in the result rather than leaving rows unwritten.
 __device__ __forceinline__ bool plan_ok(const AttnArgs& a) {
   const cev_plan_header* h = (const cev_plan_header*)a.plan;
-  return h->magic == CEV_PLAN_MAGIC && h->n_tiles == a.n_tiles && h->t == a.t && h->s_cache == a.s_cache && h->n_splits == a.n_splits;
+  return h->magic == CEV_PLAN_MAGIC && (uint32_t)h->sig == a.plan_sig && h->n_tiles == a.n_tiles && h->t == a.t &&
+         h->s_cache == a.s_cache && h->n_splits == a.n_splits;
+}
+
+// Workgroup b of the grid writes NaN over output rows [b t / G, (b+1) t / G)
+// of every query head (the launcher validated the output strides).
+template <typename T, int D>
+__device__ void poison_output(const AttnArgs& a) {
+  const int64_t G = gridDim.x;
+  const int64_t r0 = (int64_t)blockIdx.x * a.t / G, r1 = (int64_t)(blockIdx.x + 1) * a.t / G;
+  const int64_t per_row = (int64_t)a.hq * D;
+  for (int64_t i = threadIdx.x; i < (r1 - r0) * per_row; i += blockDim.x) {
+    const int64_t r = r0 + i / per_row, h = (i % per_row) / D, e = i % D;
+    ((T*)a.out)[r * a.o_st + h * a.o_sh + e] = (T)__builtin_nanf("");
+  }
 }
 
 // Clamps a segment to the key buffer it starts in.
@@ -528,7 +546,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   using namespace pipe;
   __shared__ __align__(16) char lds[2 * kBuf * kTileBytes];
 
-  if (!plan_ok(a)) return;
+  if (!plan_ok(a)) {
+    poison_output<T, D>(a);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform_i32(tid >> 6);
   const int n = lane & 31, u = lane >> 5;
   const int kvh = blockIdx.x % a.hkv;
@@ -879,7 +900,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
   using P = typename F::P;
   __shared__ __align__(16) T smem[2 * TILE];
 
-  if (!plan_ok(a)) return;
+  if (!plan_ok(a)) {
+    poison_output<T, D>(a);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, u = lane >> 5;
   const int kvh = blockIdx.x % a.hkv;
@@ -1174,10 +1198,17 @@ int32_t launch(const AttnArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-extern "C" int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q,
-                                        const void* k_cache, const void* v_cache, const void* k_new, const void* v_new, const void* gate,
-                                        void* out, void* workspace, size_t workspace_bytes, cev_stream stream) {
+namespace {
+
+// Validation and launch shared by both entry points.
+int32_t packed_attention_impl(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q, const void* k_cache,
+                              const void* v_cache, const void* k_new, const void* v_new, const void* gate, void* out, void* workspace,
+                              size_t workspace_bytes, cev_stream stream) {
   CEV_CHECK_ARG(d != nullptr, "cev_packed_attention: null descriptor");
+  // The strides, scale and gate flag of this launch are checked here, not
+  // only when the plan was built: they may change between calls.
+  int32_t drc = cev_check_attn_desc(d);
+  if (drc) return drc;
   CEV_CHECK_ARG(plan_host != nullptr && plan_dev != nullptr, "cev_packed_attention: null plan");
   const cev_plan_header* h = (const cev_plan_header*)plan_host;
   CEV_CHECK_ARG(h->magic == CEV_PLAN_MAGIC && h->version == CEV_PLAN_VERSION, "cev_packed_attention: not a plan");
@@ -1236,10 +1267,19 @@ extern "C" int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan
   a.n_splits = h->n_splits;
   a.tile_rows = h->tile_rows;
   a.scale_log2 = d->scale * 1.4426950408889634f;
+  a.plan_sig = (uint32_t)h->sig;
   hipStream_t s = (hipStream_t)stream;
   if (d->dtype == CEV_BF16) {
     if (d->head_dim == 128) return launch<__bf16, 128>(a, s);
     return launch<__bf16, 256>(a, s);
   }
   return launch<float, 128>(a, s);
+}
+
+}  // namespace
+
+extern "C" int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q,
+                                        const void* k_cache, const void* v_cache, const void* k_new, const void* v_new, const void* gate,
+                                        void* out, void* workspace, size_t workspace_bytes, cev_stream stream) {
+  return packed_attention_impl(d, plan_host, plan_dev, q, k_cache, v_cache, k_new, v_new, gate, out, workspace, workspace_bytes, stream);
 }

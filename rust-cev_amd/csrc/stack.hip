@@ -279,10 +279,12 @@ __global__ __launch_bounds__(64) void debias_kernel(DebiasArgs a) {
     const float z = lane < k ? a.logits[row + lane] : 0.0f;
     double d = log_softmax_lane(z, k, lane);
     if (a.calib) d -= log_softmax_lane(lane < k ? a.calib[row + lane] : 0.0f, k, lane);
-    const int o = lane < k ? a.order[row + lane] : 0;
-    order_ok &= o >= 0 && o < k;
-    // order is a permutation: each option gets one lane's term per variant;
-    // the barrier keeps variants in order (LDS work of one wave)
+    const int o = lane < k ? a.order[row + lane] : -1;
+    // order must be a permutation of 0..k-1: every option is named by
+    // exactly one of the k lanes (a repeated index leaves another unnamed)
+    for (int j = 0; j < k; ++j) order_ok &= __popcll(__ballot(o == j)) == 1;
+    // each option then gets one lane's term per variant; the barrier keeps
+    // variants in order (LDS work of one wave)
     if (lane < k && o >= 0 && o < k) score[o] += d / (double)n;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();

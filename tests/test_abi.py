@@ -67,6 +67,19 @@ def test_malformed_tables_are_rejected(cev, blocks, code):
     assert _abi.lib().cev_last_error()
 
 
+@pytest.mark.parametrize("blocks", [
+    [B(0, 16, 2**31 - 6)],                               # local keys end past INT32_MAX
+    [B(0, 16, 0, spans=[(2**31 - 6, 16)])],              # a span ending past INT32_MAX
+    [B(0, 16, 0, spans=[(2**31 - 1, 2**31 - 1)])],
+])
+def test_table_intervals_do_not_wrap(cev, blocks):
+    """Interval ends are formed in 64 bits: a begin near INT32_MAX plus a
+    length must be rejected, not wrap to a small end that passes."""
+    d = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 16, 0)
+    assert _plan_rc(d, blocks) == CEV_ERR_INVALID
+    assert "outside" in _abi.lib().cev_last_error().decode()
+
+
 @pytest.mark.parametrize("kw,code", [
     (dict(head_dim=64), CEV_ERR_UNSUPPORTED),
     (dict(n_q_heads=12, n_kv_heads=4), CEV_ERR_UNSUPPORTED),   # g = 3
@@ -111,6 +124,18 @@ def test_launch_validates_before_any_gpu_call(cev):
     assert L.cev_packed_attention(C.byref(d), hp, fake, fake, None, None, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
     d.has_gate = 1
     assert L.cev_packed_attention(C.byref(d), hp, fake, fake, fake, fake, fake, fake, None, fake, None, 0, None) == CEV_ERR_INVALID
+    d.has_gate = 0
+    # the launch's own strides and scale are validated, not only the plan's
+    for field, value, code in (("kc_stride_s", 100, CEV_ERR_UNSUPPORTED),   # rows not 16-byte aligned
+                               ("kc_stride_s", 64, CEV_ERR_UNSUPPORTED),    # row shorter than head_dim
+                               ("kn_stride_t", 2**40, CEV_ERR_UNSUPPORTED), # beyond a buffer load's range
+                               ("o_stride_h", -128, CEV_ERR_INVALID),
+                               ("scale", float("nan"), CEV_ERR_INVALID),
+                               ("scale", -0.5, CEV_ERR_INVALID)):
+        bad = cev_hip.attn_desc(CEV_BF16, 8, 2, 128, 8, 10)
+        setattr(bad, field, value)
+        rc = L.cev_packed_attention(C.byref(bad), hp, fake, fake, fake, fake, fake, fake, None, fake, None, 0, None)
+        assert rc == code, (field, value, rc)
 
 
 def test_empty_table_needs_no_launch(cev):

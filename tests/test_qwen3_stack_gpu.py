@@ -235,3 +235,9 @@ def test_debias_position_invariant_model_and_invalid_spans(gpu):
     broken[begin[1], 0] = 2  # k = 2: option index out of range
     got = _device_debias(gpu, logits, broken, begin, length, kk)
     assert np.isnan(got[1, :2]).all() and np.isfinite(got[0, :5]).all() and np.isfinite(got[2, :8]).all()
+    # a repeated index (every entry in range, option 1 never named) is not a
+    # permutation either
+    dup = order.copy()
+    dup[begin[2] + 1, :8] = [0, 0, 2, 3, 4, 5, 6, 7]
+    got = _device_debias(gpu, logits, dup, begin, length, kk)
+    assert np.isnan(got[2, :8]).all() and np.isfinite(got[0, :5]).all() and np.isfinite(got[1, :2]).all()
