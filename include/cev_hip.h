@@ -148,6 +148,22 @@ int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan_host, cons
                              const void* v_cache, const void* k_new, const void* v_new, const void* gate, void* out, void* workspace,
                              size_t workspace_bytes, cev_stream stream);
 
+/* Allocation-free variant of cev_packed_attention, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, hosts that forbid hipMalloc).  It has no counterpart in the
+ * reference.  Same arguments, results and validation as
+ * cev_packed_attention, but a split plan's partial records go to a static
+ * device buffer of CEV_ATTN_SCRATCH_BYTES inside the library (one per GPU,
+ * held until the process ends) instead of a caller workspace: a plan whose
+ * cev_attn_workspace_size exceeds it fails with CEV_ERR_SPACE.  It calls no
+ * hipMalloc / hipFree.  Every call on one GPU shares that buffer: calls
+ * that overlap in time on one GPU (several streams or threads) race and
+ * must be serialised by the caller. */
+#define CEV_ATTN_SCRATCH_BYTES ((size_t)64 << 20)
+int32_t cev_packed_attention_noalloc(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q,
+                                     const void* k_cache, const void* v_cache, const void* k_new, const void* v_new, const void* gate,
+                                     void* out, cev_stream stream);
+
 /* ------------------------------------------------------------------ */
 /* Fused QK RMSNorm + RoPE with per-token positions: replaces
  * q_norm / k_norm + Rotary::apply of qwen3.rs:193-196 and the Qwen3.5 form

@@ -20,6 +20,7 @@ CEV_ERR_SPACE = -4
 CEV_F32 = 0
 CEV_BF16 = 1
 CEV_MAX_SPANS = 4
+CEV_ATTN_SCRATCH_BYTES = 64 << 20
 
 i32 = C.c_int32
 i64 = C.c_int64
@@ -95,6 +96,7 @@ SIGNATURES = {
     "cev_attn_plan_build": (i32, [C.POINTER(AttnDesc), PBlock, i32, P, C.c_size_t]),
     "cev_attn_workspace_size": (i32, [P, C.POINTER(C.c_size_t)]),
     "cev_packed_attention": (i32, [C.POINTER(AttnDesc), P, P, P, P, P, P, P, P, P, P, C.c_size_t, P]),
+    "cev_packed_attention_noalloc": (i32, [C.POINTER(AttnDesc), P, P, P, P, P, P, P, P, P, P]),
     "cev_qknorm_desc_init": (i32, [C.POINTER(QkNormDesc), i32, i32, i32, i32, i32, i32, i32, i32, C.c_float, i32]),
     "cev_qknorm_rope": (i32, [C.POINTER(QkNormDesc), P, P, P, P, P, P, P, P, P, P]),
     "cev_rope_table": (i32, [C.c_double, i32, i32, i32, P, P]),

@@ -23,6 +23,8 @@
 //     KV head and its K/V stream stays in that XCD's L2;
 //   - a split tile writes (unnormalised O, m, l) per row and head to the
 //     workspace and attn_merge_kernel combines the parts.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "cev_device.h"
@@ -1198,6 +1200,13 @@ int32_t launch(const AttnArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+// Scratch of the allocation-free entry point: the split-KV partial records
+// (f32 O, m, l per row, head and part).  Every record a merge reads is
+// written by the same call first, so nothing in it has to start at zero.
+// Each GPU the library runs on holds its own copy until the process ends.
+constexpr size_t kScratchBytes = CEV_ATTN_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
 namespace {
 
 // Validation and launch shared by both entry points.
@@ -1276,10 +1285,57 @@ int32_t packed_attention_impl(const cev_attn_desc* d, const void* plan_host, con
   return launch<float, 128>(a, s);
 }
 
+// Device addresses of `scratch` (below), one per device, looked up once with that
+// device current.  The array's name in host code is only a stand-in for
+// the symbol and is never passed to a kernel.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int32_t scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return cev_fail(CEV_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", dev, kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) return cev_fail(CEV_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return CEV_OK;
+}
+
 }  // namespace
 
 extern "C" int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q,
                                         const void* k_cache, const void* v_cache, const void* k_new, const void* v_new, const void* gate,
                                         void* out, void* workspace, size_t workspace_bytes, cev_stream stream) {
   return packed_attention_impl(d, plan_host, plan_dev, q, k_cache, v_cache, k_new, v_new, gate, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int32_t cev_packed_attention_noalloc(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q,
+                                                const void* k_cache, const void* v_cache, const void* k_new, const void* v_new,
+                                                const void* gate, void* out, cev_stream stream) {
+  CEV_CHECK_ARG(plan_host != nullptr, "cev_packed_attention_noalloc: null plan");
+  const cev_plan_header* h = (const cev_plan_header*)plan_host;
+  CEV_CHECK_ARG(h->magic == CEV_PLAN_MAGIC && h->version == CEV_PLAN_VERSION, "cev_packed_attention_noalloc: not a plan");
+  size_t need = 0;
+  int32_t rc = cev_attn_workspace_size(plan_host, &need);
+  if (rc) return rc;
+  if (need > kScratchBytes)
+    return cev_fail(CEV_ERR_SPACE, "cev_packed_attention_noalloc: the plan needs %zu bytes of split records, the static scratch holds %zu",
+                    need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    rc = scratch_ptr(&ws);
+    if (rc) return rc;
+  }
+  return packed_attention_impl(d, plan_host, plan_dev, q, k_cache, v_cache, k_new, v_new, gate, out, ws, need > 0 ? kScratchBytes : 0,
+                               stream);
 }
