@@ -4,14 +4,15 @@
 A step is one pass of the hot path over the workload's packed suffix with
 every input resident in HBM: K1 (QK RMSNorm + RoPE with per-block position
 restart) then K2 (packed attention over the cached prefix and the suffix
-blocks).  The default workload is the 32k-prefix packed-prefill shape: a
+blocks), and for the d3 workload (c4) the readout of the last position.  The default workload is the 32k-prefix packed-prefill shape: a
 Qwen3-8B-shaped layer (Hq=32, Hkv=8, d=128, bf16) with 64 suffix blocks x 64
 tokens after a 32768-token cached prefix.
 
 Prints one JSON line: query tokens/s (value), TFLOP/s, the roofline record of
-K2 (its average launch time from HIP events on its stream) and the CPU
-baseline (the oracle's candle-op restatement on a bounded sample, timed on
-this host's cores).
+K2 (its average launch time from HIP events on its stream), the CPU baseline
+(the oracle's candle-op restatement on a bounded sample, timed on this
+host's cores) and, for the default workload, K2 on the HBM-bound
+32k-prefix x 16-token shape under hbm_shape (outside the timed steps).
 """
 import argparse
 import json
@@ -311,27 +312,25 @@ def bench_stack(args, w, dev):
     stack = Qwen3Stack(w, w.device_weights(dev, dtype), dev, capacity=w.state_tokens + w.questions * w.q_len)
     torch.cuda.empty_cache()
     state, qs, codes = w.ids()
-    stack.prefill(state[: w.head_tokens], w.prefill_chunk)  # warm-up (library GEMM selection)
-    stack.cached = 0
+    # the head is prefilled into slots [0, head) (engine.rs:247-256); the
+    # pass computes the tail into [head, state) and the questions into the
+    # slots after it
+    stack.prefill(0, state[: w.head_tokens], w.prefill_chunk)  # warm-up (library GEMM selection)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    stack.prefill(state[: w.head_tokens], w.prefill_chunk)
+    stack.prefill(0, state[: w.head_tokens], w.prefill_chunk)
     e1.record()
     torch.cuda.synchronize()
     prefill_ms = e0.elapsed_time(e1)
-    plans, items = w.plans_items()
-    table, pos, gather = BlockTable.from_plans(plans, items)
+    items = [(0, w.q_len, w.state_tokens + k * w.q_len) for k in range(w.questions)]
+    table, pos, slots, gather = BlockTable.from_slots([(0, w.state_tokens, w.head_tokens)], items, stack.capacity)
     tokens = np.concatenate([state[w.head_tokens:], qs.reshape(-1)])
 
-    tail = w.state_tokens - w.head_tokens
-
     def step():
-        # The pass keeps its tail's K/V in the cache, as forward_packed does;
-        # the cache length is then reset so every step repeats the same pass.
-        logits = stack.code_logits(stack.forward_packed(tokens, pos, table, gather, keep_tokens=tail), codes)
-        stack.cached -= tail
-        return logits
+        # one packed pass (the tail lands in its slots again, with the same
+        # values) and the code-head logits
+        return stack.code_logits(stack.hidden(stack.run(tokens, pos, slots, table), gather), codes)
 
     for _ in range(args.warmup):
         step()
@@ -373,6 +372,50 @@ def bench_stack(args, w, dev):
     print(json.dumps(res), flush=True)
 
 
+def time_layer(layer, steps: int, warmup: int, graph: bool):
+    """Times `steps` steps of one attention layer: K1, K2 and, for a d3
+    workload, the readout of the last position, each bracketed by HIP events
+    on the stream they launch on.  Returns (ms per step by the host clock,
+    mean K1 ms, mean K2 ms, mean readout ms or None)."""
+    import torch
+    parts = [layer.qknorm, layer.attend] + ([layer.read_out] if layer.readout is not None else [])
+    for _ in range(warmup):
+        for f in parts:
+            f()
+    torch.cuda.synchronize()
+    if graph:
+        parts = [g.replay for g in capture(parts)]
+        for _ in range(warmup):
+            for f in parts:
+                f()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(parts) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        for j, f in enumerate(parts):
+            f()
+            ev[i][j + 1].record()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / steps
+    means = [statistics.mean(e[j].elapsed_time(e[j + 1]) for e in ev) for j in range(len(parts))]
+    return ms_step, means[0], means[1], (means[2] if len(means) > 2 else None)
+
+
+def hbm_shape_record(dev, steps: int, warmup: int):
+    """K2 on the long-prefix short-suffix shape (the 32768-key prefix with one
+    16-token block), where the kernel streams K/V and HBM bandwidth bounds
+    it: its mean time and the fraction of the 8 TB/s peak."""
+    from cev_hip import configs
+    from cev_hip.layer import AttentionLayer
+    w = configs.hbm(1)
+    _, k1_ms, k2_ms, _ = time_layer(AttentionLayer(w, dev), steps, warmup, False)
+    gbps = w.alg_bytes() / (k2_ms * 1e-3) / 1e9
+    return {"workload": f"{w.name}: {w.notes}", "k1_ms": k1_ms, "k2_ms": k2_ms, "alg_bytes": w.alg_bytes(),
+            "achieved_gbps": gbps, "peak_gbps": PEAK_HBM_GBPS, "frac": gbps / PEAK_HBM_GBPS,
+            "kernel": "attn_kernel_pipe<bf16,128> (split) + attn_merge_kernel"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -382,6 +425,9 @@ def main():
                     help="c3 (default): the 32k-prefix packed-prefill attention; c2: the Qwen3-1.7B-shaped stack's packed "
                          "pass; c5gdn / c5gdnrows: the Gated DeltaNet layer core over one 4096-token row / 32 rows of 64 tokens")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline leg")
+    ap.add_argument("--hbm-shape", type=int, default=1,
+                    help="with the default c3 workload, also time K2 on the 32k-prefix x 16-token shape (HBM-bound) "
+                         "and report it under hbm_shape; 0 skips it")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: capture each timed call once in a HIP graph and replay it; 0 (default): launch directly (graph launch costs more than it saves here)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -425,31 +471,7 @@ def main():
         return
     w = configs.WORKLOADS[args.workload]()
     layer = AttentionLayer(w, dev)
-    for _ in range(args.warmup):
-        layer.forward()
-    torch.cuda.synchronize()
-    k1, k2 = layer.qknorm, layer.attend
-    if args.graph:
-        g1, g2 = capture([k1, k2])
-        k1, k2 = g1.replay, g2.replay
-        for _ in range(args.warmup):
-            k1()
-            k2()
-
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record()
-        k1()
-        ev[i][1].record()
-        k2()
-        ev[i][2].record()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    k1_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in ev)
-    k2_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in ev)
+    ms_step, k1_ms, k2_ms, k3_ms = time_layer(layer, args.steps, args.warmup, args.graph)
 
     dtype = "bf16" if w.bf16 else "f32"
     flops = w.useful_flops()
@@ -482,6 +504,13 @@ def main():
         "roofline": roof,
         "device": device_info().name,
     }
+    if k3_ms is not None:
+        hidden, codes, temp = w.readout
+        res["readout_ms"] = k3_ms
+        res["config"]["readout"] = (f"d3 Kind::Matrix at the last position: o_proj ({w.hq * w.d} -> {hidden}), f32, "
+                                    f"{codes} x {hidden} readout / temperature {temp}")
+    if args.workload == "c3" and args.hbm_shape:
+        res["hbm_shape"] = hbm_shape_record(dev, args.steps, args.warmup)
     if args.cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, layer.np_inputs)
     print(json.dumps(res), flush=True)

@@ -193,6 +193,19 @@ int32_t cev_qknorm_desc_init(cev_qknorm_desc* d, int32_t dtype, int32_t n_q_head
 int32_t cev_qknorm_rope(const cev_qknorm_desc* d, const void* q_in, const void* k_in, const void* w_q, const void* w_k, const int32_t* pos,
                         const void* cos, const void* sin, void* q_out, void* k_out, cev_stream stream);
 
+/* cev_qknorm_rope plus the KV-cache store of the new tokens
+ * (qwen3.rs:193-200 / qwen35.rs:536-544 up to the cat): q as above; the
+ * normalised, rotated k row of token i and its v row (copied unchanged from
+ * v_in (t, hkv, d) with strides vi_stride_t / vi_stride_h) are written to row
+ * slots[i] of k_out and of v_out (strides ko_* and vo_stride_t /
+ * vo_stride_h), e.g. a token's slot in a (hkv, capacity, d) cache.  slots
+ * NULL writes row i; a slot outside [0, n_slots) stores neither row.  v rows
+ * 16-byte aligned.  One launch. */
+int32_t cev_qknorm_rope_kv(const cev_qknorm_desc* d, const void* q_in, const void* k_in, const void* v_in, int64_t vi_stride_t,
+                           int64_t vi_stride_h, const void* w_q, const void* w_k, const int32_t* pos, const void* cos, const void* sin,
+                           const int32_t* slots, int32_t n_slots, void* q_out, void* k_out, void* v_out, int64_t vo_stride_t,
+                           int64_t vo_stride_h, cev_stream stream);
+
 /* RoPE cos/sin table exactly as Rotary::new builds it (qwen3.rs:107-118):
  * inv_i = 1 / (theta^(2i/rotary_dim) in f64, rounded to f32), angle =
  * f32(p) * inv_i in f32, cos/sin in f32, then rounded to dtype.  Host only;
@@ -280,6 +293,39 @@ int32_t cev_debias_scores(int32_t n_questions, int32_t n_variants, const int32_t
                           const int32_t* n_options, const float* logits, const float* calib, const int32_t* order, int32_t ld,
                           float* scores, cev_stream stream);
 
+/* Linear layers and row gathers (the candle ops around the attention call
+ * in the device-resident stack and the readouts).
+ *
+ * cev_blas is a hipBLASLt context for products of more than 8 rows; it
+ * caches one algorithm per problem shape.  Use a handle from one thread at a
+ * time. */
+typedef void* cev_blas;
+int32_t cev_blas_create(cev_blas* handle);
+int32_t cev_blas_destroy(cev_blas handle);
+
+/* y = out_dtype(alpha * x . w^T): Linear::forward without bias
+ * (crates/cev-model/src/qwen3.rs:175-178, :229-233), the code head
+ * hidden . code_head^T (engine.rs:463) and the d3 readout
+ * answers . weight^T / temperature (hybrid.rs:657, alpha = 1 / temperature
+ * rounded to f32).  x (m, k) row stride ldx, w (n, k) row stride ldw, y (m, n)
+ * row stride ldy, all row-major; x and w in `dtype`, y in out_dtype (CEV_F32
+ * or dtype); f32 accumulation, one rounding to the output dtype.  m <= 8
+ * runs this library's own kernel (handle may be NULL, no workspace); larger
+ * m a hipBLASLt GEMM on `handle` with the caller's workspace
+ * (CEV_LINEAR_WORKSPACE_BYTES recommended; 0 allowed). */
+#define CEV_LINEAR_WORKSPACE_BYTES ((size_t)32 << 20)
+int32_t cev_linear(cev_blas handle, int32_t dtype, int32_t out_dtype, int64_t m, int64_t n, int64_t k, const void* x, int64_t ldx,
+                   const void* w, int64_t ldw, float alpha, void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                   cev_stream stream);
+
+/* out[i] = out_dtype(table[ids[i]]) for i < n, rows of `width` elements:
+ * Embedding::forward's rows (qwen3.rs:288-293), index_select of the answer
+ * rows (qwen3.rs:399), to_dtype(F32) (qwen3.rs:400, ids NULL = identity)
+ * and the code head's rows of the tied embedding (engine.rs:155).  ids is
+ * a device int32 array; an id outside [0, table_rows) gives a NaN row. */
+int32_t cev_gather_rows(int32_t dtype, int32_t out_dtype, int64_t n, int64_t width, const void* table, int64_t ld_table, int64_t table_rows,
+                        const int32_t* ids, void* out, int64_t ld_out, cev_stream stream);
+
 /* ------------------------------------------------------------------ */
 /* Table builders (host only). */
 
@@ -296,6 +342,49 @@ int32_t cev_debias_scores(int32_t n_questions, int32_t n_variants, const int32_t
 int32_t cev_table_from_plans(int32_t n_plans, const int32_t* past_len, const int32_t* prefix_len, const int32_t* tail_start, int32_t n_items,
                              const int32_t* item_plan, const int32_t* item_len, cev_block* blocks, int32_t max_blocks, int32_t* n_out_blocks,
                              int32_t* pos, int32_t max_tokens, int32_t* n_tokens, int32_t* gather);
+
+/* The packed pass of engine.rs:365-442 over slot-addressed K/V caches (a
+ * cev_prefix_store): keys are cache slots, so a plan's past is read where
+ * it lies and its tail is written next to it (no cat, engine.rs:375-387,
+ * :449-457).  Plan p's prefix occupies slots [kv_begin[p], kv_begin[p] +
+ * prefix_len[p]), its first tail_start[p] tokens already computed; the
+ * rest (its tail) is computed by this pass.  Question k's tokens take slots
+ * item_slot[k] .. + item_len[k] - 1.  Token order, positions (restarting
+ * at prefix_len per question, engine.rs:411) and gather are those of
+ * cev_table_from_plans; slots[i] receives the cache slot of pass token i
+ * (for cev_qknorm_rope_kv).  Attend with s_cache = capacity (every key is a
+ * cache slot) and t = *n_tokens.  A written slot range that overlaps any
+ * other range of the pass is rejected.  A chunk of a prefix's prefill is a
+ * plan with no questions whose tail is the chunk (qwen3.rs:346-362). */
+int32_t cev_table_from_slots(int32_t n_plans, const int32_t* kv_begin, const int32_t* prefix_len, const int32_t* tail_start, int32_t n_items,
+                             const int32_t* item_plan, const int32_t* item_len, const int32_t* item_slot, int32_t capacity, cev_block* blocks,
+                             int32_t max_blocks, int32_t* n_out_blocks, int32_t* pos, int32_t* slots, int32_t max_tokens, int32_t* n_tokens,
+                             int32_t* gather);
+
+/* Device prefix store: the engine's PrefixCache (engine.rs:474-503) over
+ * slot ranges of per-layer (hkv, capacity, d) device caches that the caller
+ * owns; host bookkeeping only, thread-safe.  LRU by total cached tokens
+ * (budget) with PrefixCache's get / put semantics; a range a pass holds
+ * (get hit or reserve) stays allocated until released, also if evicted
+ * meanwhile.  When no free run fits a reservation the oldest unheld entries
+ * are evicted until one does; CEV_ERR_SPACE if none fits even then. */
+typedef void* cev_prefix_store;
+int32_t cev_prefix_store_create(int32_t capacity, int64_t budget, cev_prefix_store* store);
+int32_t cev_prefix_store_destroy(cev_prefix_store store);
+/* PrefixCache::get: *found = 1 and *begin = its first slot on a hit (now
+ * most recently used, and held until released). */
+int32_t cev_prefix_store_get(cev_prefix_store store, const uint32_t* tokens, int32_t n, int32_t* begin, int32_t* found);
+/* n contiguous slots for this pass (a prefix being computed, question
+ * tokens), held until released. */
+int32_t cev_prefix_store_reserve(cev_prefix_store store, int32_t n, int32_t* begin);
+/* PrefixCache::put of a held reservation of exactly n slots holding the
+ * K/V of `tokens`; a key longer than the budget is not cached. */
+int32_t cev_prefix_store_put(cev_prefix_store store, const uint32_t* tokens, int32_t n, int32_t begin);
+int32_t cev_prefix_store_release(cev_prefix_store store, int32_t begin);
+/* Entries, their total key length and the slots in use (entries + held). */
+int32_t cev_prefix_store_stats(cev_prefix_store store, int32_t* entries, int64_t* cached_tokens, int32_t* used_slots);
+/* Entry i in LRU order (0 = oldest): its first slot and length. */
+int32_t cev_prefix_store_entry(cev_prefix_store store, int32_t i, int32_t* begin, int32_t* len);
 
 /* Rows of a batch (HybridEngine::rows, hybrid.rs:592-617): b rows of t
  * tokens packed row-major.  causal != 0: each row continues `past` cached

@@ -44,10 +44,12 @@ class Qwen3Oracle:
         self.past = [(np.zeros((w.hkv, 0, w.d), np.float32), np.zeros((w.hkv, 0, w.d), np.float32)) for _ in range(w.n_layers)]
         self.cos, self.sin = rope_table(w.theta, w.d, w.state_tokens + w.questions * w.q_len + 1, self.bf)
 
-    def _layers(self, tokens, pos, mask):
-        """All layers over new tokens with the dense additive mask (t, past + t).
+    def _layers(self, tokens, pos, mask, past=None):
+        """All layers over new tokens with the dense additive mask (t, past + t)
+        over `past` (per layer (k, v), default the oracle's own cache).
         Returns the last residual stream and each layer's new (k, v)."""
         w, W, bf = self.w, self.W, self.bf
+        past = self.past if past is None else past
         t = len(tokens)
         H, hq, hkv, d = w.hidden, w.hq, w.hkv, w.d
         x = W["embed"][np.asarray(tokens, np.int64)].astype(np.float32)
@@ -61,7 +63,7 @@ class Qwen3Oracle:
             q = rope(rms_norm(q, W[p + "q_norm"], w.eps, bf), pos, self.cos, self.sin, d, bf)
             k = rope(rms_norm(k, W[p + "k_norm"], w.eps, bf), pos, self.cos, self.sin, d, bf)
             kt, vt = k.transpose(1, 0, 2), v.transpose(1, 0, 2)
-            pk, pv = self.past[i]
+            pk, pv = past[i]
             kall = np.ascontiguousarray(np.concatenate([pk, kt], axis=1))
             vall = np.ascontiguousarray(np.concatenate([pv, vt], axis=1))
             a = attend(np.ascontiguousarray(q.transpose(1, 0, 2)), kall, vall, mask, bf)[0]  # (hq, t, d)
@@ -93,6 +95,18 @@ class Qwen3Oracle:
         self.past = [(np.concatenate([pk, k[:, :tail]], 1), np.concatenate([pv, v[:, :tail]], 1))
                      for (pk, pv), (k, v) in zip(self.past, kv)]
         return hid
+
+    def prefill_kv(self, tokens, chunk: int):
+        """Qwen3::prefill from an empty cache, returned as per-layer (k, v)
+        instead of kept (the PrefixKv the engine caches, engine.rs:251-254)."""
+        kv = [(np.zeros((self.w.hkv, 0, self.w.d), np.float32),) * 2 for _ in range(self.w.n_layers)]
+        for c0 in range(0, len(tokens), max(1, chunk)):
+            part = tokens[c0: c0 + chunk]
+            n, past = len(part), kv[0][0].shape[1]
+            mask = segment_mask(np.zeros(n, np.uint32), past)
+            _, new = self._layers(part, np.arange(past, past + n, dtype=np.int32), mask, past=kv)
+            kv = [(np.concatenate([pk, k], 1), np.concatenate([pv, v], 1)) for (pk, pv), (k, v) in zip(kv, new)]
+        return kv
 
     def code_logits(self, hidden, code_ids):
         head = self.W["embed"][np.asarray(code_ids, np.int64)].astype(np.float32)

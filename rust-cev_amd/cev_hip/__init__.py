@@ -17,12 +17,14 @@ from typing import Optional, Sequence
 import numpy as np
 
 from . import synth  # noqa: F401  (re-exported)
-from ._abi import (CEV_BF16, CEV_F32, CEV_MAX_SPANS, AttnDesc, Block, CevError, GdnDesc, QkNormDesc, Span, check, lib)
+from ._abi import (CEV_BF16, CEV_F32, CEV_LINEAR_WORKSPACE_BYTES, CEV_MAX_SPANS, AttnDesc, Block, CevError, GdnDesc, QkNormDesc, Span,
+                   check, lib)
 
 __all__ = [
     "GatedDeltaNet",
     "CEV_BF16", "CEV_F32", "CevError", "Block", "Span", "BlockTable", "AttnPlan", "PackedAttention",
     "packed_attention", "qknorm_rope", "rope_table", "Rotary", "device_info", "synth",
+    "Blas", "linear", "gather_rows", "D3Readout", "PrefixStore", "qknorm_rope_kv",
 ]
 
 
@@ -103,6 +105,28 @@ class BlockTable:
         s_cache = int(sum(p[0] for p in plans))
         tab = cls([blocks[i] for i in range(nb.value)], nt.value, s_cache)
         return tab, np.frombuffer(pos, np.int32)[: nt.value].copy(), np.frombuffer(gather, np.int32)[: len(items)].copy()
+
+    @classmethod
+    def from_slots(cls, plans, items, capacity: int):
+        """engine.rs:365-442 over slot-addressed caches.  plans: [(kv_begin,
+        prefix_len, tail_start)]; items: [(plan, question_len, first_slot)].
+        Returns (table with s_cache = capacity, pos, slots, gather)."""
+        L = lib()
+        a = lambda xs: (C.c_int32 * max(1, len(xs)))(*[int(x) for x in xs])  # noqa: E731
+        kb, pre, ts = a([p[0] for p in plans]), a([p[1] for p in plans]), a([p[2] for p in plans])
+        ip, il, isl = a([i[0] for i in items]), a([i[1] for i in items]), a([i[2] for i in items])
+        nb, nt = C.c_int32(), C.c_int32()
+        check(L.cev_table_from_slots(len(plans), kb, pre, ts, len(items), ip, il, isl, int(capacity), None, 0, C.byref(nb), None, None,
+                                     0, C.byref(nt), None))
+        blocks = (Block * max(1, nb.value))()
+        pos = (C.c_int32 * max(1, nt.value))()
+        slots = (C.c_int32 * max(1, nt.value))()
+        gather = (C.c_int32 * max(1, len(items)))()
+        check(L.cev_table_from_slots(len(plans), kb, pre, ts, len(items), ip, il, isl, int(capacity), blocks, nb.value, C.byref(nb), pos,
+                                     slots, nt.value, C.byref(nt), gather))
+        tab = cls([blocks[i] for i in range(nb.value)], nt.value, int(capacity))
+        as_np = lambda x, n: np.frombuffer(x, np.int32)[:n].copy()  # noqa: E731
+        return tab, as_np(pos, nt.value), as_np(slots, nt.value), as_np(gather, len(items))
 
     @classmethod
     def from_rows(cls, b: int, t: int, past: int = 0, causal: bool = True, lengths=None):
@@ -318,6 +342,33 @@ def qknorm_rope(q_in, k_in, w_q, w_k, pos, rot: Rotary, eps: float, plus_one: bo
     return q_out, k_out
 
 
+def qknorm_rope_kv(q_in, k_in, v_in, w_q, w_k, pos, rot: Rotary, eps: float, q_out, k_out, v_out, slots=None, n_slots: int = 0,
+                   plus_one: bool = False, stream=None):
+    """qknorm_rope plus the cache store of the new tokens in one launch: k
+    (normalised, rotated) and v (copied) of token i land in row slots[i] of
+    k_out / v_out (row i without slots), e.g. (t_or_capacity, hkv, d) views
+    of head-major caches."""
+    torch = _torch()
+    t, hq, d = q_in.shape
+    hkv = k_in.shape[1]
+    code = _dtype_code(q_in)
+    desc = QkNormDesc()
+    check(lib().cev_qknorm_desc_init(C.byref(desc), code, hq, hkv, d, t, rot.rotary_dim, rot.n_pos, 1 if plus_one else 0, float(eps), 0))
+    for t_ in (q_in, k_in, v_in, q_out, k_out, v_out):
+        if t_.stride(-1) != 1:
+            raise CevError(-2, "last dimension must be contiguous")
+    desc.qi_stride_t, desc.qi_stride_h = q_in.stride(0), q_in.stride(1)
+    desc.ki_stride_t, desc.ki_stride_h = k_in.stride(0), k_in.stride(1)
+    desc.qo_stride_t, desc.qo_stride_h = q_out.stride(0), q_out.stride(1)
+    desc.ko_stride_t, desc.ko_stride_h = k_out.stride(0), k_out.stride(1)
+    if pos.dtype != torch.int32 or (slots is not None and slots.dtype != torch.int32):
+        raise CevError(-1, "positions and slots must be int32")
+    check(lib().cev_qknorm_rope_kv(C.byref(desc), _ptr(q_in), _ptr(k_in), _ptr(v_in), v_in.stride(0), v_in.stride(1), _ptr(w_q),
+                                   _ptr(w_k), _ptr(pos), _ptr(rot.cos), _ptr(rot.sin), _ptr(slots), int(n_slots), _ptr(q_out),
+                                   _ptr(k_out), _ptr(v_out), v_out.stride(0), v_out.stride(1), _stream_ptr(stream)))
+    return q_out, k_out, v_out
+
+
 def rms_norm(x, w, eps: float, h=None, x_out=None, y=None, plus_one: bool = False, stream=None):
     """candle_nn RmsNorm over the last dim of a (rows, hidden) view in the
     model dtype (qwen3.rs:254-255, :400); with h, the residual add before it
@@ -373,6 +424,165 @@ def debias_scores(logits, order, span_begin, span_len, n_options, calib=None, st
     check(lib().cev_debias_scores(n_q, n_var, _ptr(span_begin), _ptr(span_len), _ptr(n_options), _ptr(logits),
                                   _ptr(calib) if calib is not None else None, _ptr(order), ld, _ptr(scores), _stream_ptr(stream)))
     return scores
+
+
+# ---------------------------------------------------------------------------
+# Linear layers, row gathers and the d3 readout
+
+
+class Blas:
+    """A cev_blas context (hipBLASLt, cached algorithms) and its workspace on
+    one device; Blas.on(device) keeps one per device."""
+    _per_device: dict = {}
+
+    def __init__(self, device):
+        torch = _torch()
+        h = C.c_void_p()
+        check(lib().cev_blas_create(C.byref(h)))
+        self.handle = h
+        self.workspace = torch.empty(CEV_LINEAR_WORKSPACE_BYTES, dtype=torch.uint8, device=device)
+
+    @classmethod
+    def on(cls, device) -> "Blas":
+        torch = _torch()
+        key = torch.device(device).index or 0
+        if key not in cls._per_device:
+            cls._per_device[key] = cls(device)
+        return cls._per_device[key]
+
+    def __del__(self):
+        if getattr(self, "handle", None) is not None:
+            try:
+                lib().cev_blas_destroy(self.handle)
+            except Exception:  # interpreter shutdown
+                pass
+
+
+def linear(x, w, out=None, alpha: float = 1.0, out_dtype=None, blas: Optional[Blas] = None, stream=None):
+    """out = out_dtype(alpha * x @ w.T) for x (m, k), w (n, k): candle's bias-free
+    Linear::forward (qwen3.rs:175-178, :229-233), the code head (engine.rs:463)
+    and the d3 readout (hybrid.rs:657, alpha = 1 / temperature)."""
+    torch = _torch()
+    m, k = x.shape
+    n = w.shape[0]
+    code = _dtype_code(x)
+    if w.dtype != x.dtype or w.shape[1] != k:
+        raise CevError(-1, "linear: w must be (n, k) in x's dtype")
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    for t_ in (x, w, out):
+        if t_.stride(-1) != 1:
+            raise CevError(-2, "linear: last dimension must be contiguous")
+    blas = Blas.on(x.device) if (blas is None and m > 8) else blas
+    ws = blas.workspace if blas is not None else None
+    check(lib().cev_linear(blas.handle if blas is not None else None, code, _dtype_code(out), m, n, k, _ptr(x), x.stride(0), _ptr(w),
+                           w.stride(0), float(alpha), _ptr(out), out.stride(0), _ptr(ws), ws.numel() if ws is not None else 0,
+                           _stream_ptr(stream)))
+    return out
+
+
+def gather_rows(table, ids=None, out=None, out_dtype=None, stream=None):
+    """out[i] = table[ids[i]] converted to out_dtype (Embedding rows,
+    qwen3.rs:288-293; index_select of answer rows, qwen3.rs:399;
+    to_dtype(F32), qwen3.rs:400, with ids None)."""
+    torch = _torch()
+    rows, width = table.shape
+    n = rows if ids is None else ids.shape[0]
+    if ids is not None and (ids.dtype != torch.int32 or not ids.is_contiguous()):
+        raise CevError(-1, "gather_rows: ids must be contiguous int32")
+    out_dtype = table.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((n, width), dtype=out_dtype, device=table.device)
+    check(lib().cev_gather_rows(_dtype_code(table), _dtype_code(out), n, width, _ptr(table), table.stride(0), rows, _ptr(ids), _ptr(out),
+                                out.stride(0), _stream_ptr(stream)))
+    return out
+
+
+class D3Readout:
+    """Kind::Matrix (hybrid.rs:59-63, :657) over one Qwen3.5 gated-attention
+    layer: the answer rows of the gated attention output go through o_proj
+    (qwen35.rs:560, model dtype), are converted to f32 and multiplied by the
+    (codes, hidden) f32 readout matrix, then divided by the temperature
+    (candle's affine by 1 / temperature in f32)."""
+
+    def __init__(self, wo, wr, temperature: float, device, dtype):
+        torch = _torch()
+        dev = lambda x, dt: torch.from_numpy(np.ascontiguousarray(x)).to(device=device, dtype=dt)  # noqa: E731
+        self.wo = dev(wo, dtype)
+        self.wr = dev(wr, torch.float32)
+        self.alpha = float(np.float32(1.0 / np.float64(np.float32(temperature))))
+        self.h = torch.empty((1, self.wo.shape[0]), dtype=dtype, device=device)
+        self.h32 = torch.empty((1, self.wo.shape[0]), dtype=torch.float32, device=device)
+        self.logits = torch.empty((1, self.wr.shape[0]), dtype=torch.float32, device=device)
+
+    def __call__(self, rows, stream=None):
+        """rows: (r, hq d) answer rows of the attention output (r <= 8 reuse
+        the preallocated buffers); returns (r, codes) f32 logits."""
+        torch = _torch()
+        r = rows.shape[0]
+        if r != self.h.shape[0]:
+            self.h = torch.empty((r, self.wo.shape[0]), dtype=self.wo.dtype, device=rows.device)
+            self.h32 = torch.empty((r, self.wo.shape[0]), dtype=torch.float32, device=rows.device)
+            self.logits = torch.empty((r, self.wr.shape[0]), dtype=torch.float32, device=rows.device)
+        linear(rows, self.wo, out=self.h, stream=stream)
+        gather_rows(self.h, out=self.h32, stream=stream)
+        return linear(self.h32, self.wr, out=self.logits, alpha=self.alpha, stream=stream)
+
+
+class PrefixStore:
+    """cev_prefix_store: PrefixCache (engine.rs:474-503) over slot ranges of
+    the per-layer device caches."""
+
+    def __init__(self, capacity: int, budget: int):
+        h = C.c_void_p()
+        check(lib().cev_prefix_store_create(int(capacity), int(budget), C.byref(h)))
+        self.handle, self.capacity, self.budget = h, int(capacity), int(budget)
+
+    def __del__(self):
+        if getattr(self, "handle", None) is not None:
+            try:
+                lib().cev_prefix_store_destroy(self.handle)
+            except Exception:  # interpreter shutdown
+                pass
+
+    @staticmethod
+    def _ids(tokens):
+        arr = np.ascontiguousarray(tokens, np.uint32)
+        return arr, arr.ctypes.data_as(C.POINTER(C.c_uint32))
+
+    def get(self, tokens) -> Optional[int]:
+        """First slot of the cached prefix `tokens` (now held), or None."""
+        arr, p = self._ids(tokens)
+        b, f = C.c_int32(), C.c_int32()
+        check(lib().cev_prefix_store_get(self.handle, p, arr.size, C.byref(b), C.byref(f)))
+        return b.value if f.value else None
+
+    def reserve(self, n: int) -> int:
+        b = C.c_int32()
+        check(lib().cev_prefix_store_reserve(self.handle, int(n), C.byref(b)))
+        return b.value
+
+    def put(self, tokens, begin: int) -> None:
+        arr, p = self._ids(tokens)
+        check(lib().cev_prefix_store_put(self.handle, p, arr.size, int(begin)))
+
+    def release(self, begin: int) -> None:
+        check(lib().cev_prefix_store_release(self.handle, int(begin)))
+
+    def stats(self):
+        e, c, u = C.c_int32(), C.c_int64(), C.c_int32()
+        check(lib().cev_prefix_store_stats(self.handle, C.byref(e), C.byref(c), C.byref(u)))
+        return dict(entries=e.value, cached_tokens=c.value, used_slots=u.value)
+
+    def entries(self):
+        """[(first slot, length)] in LRU order (oldest first)."""
+        out = []
+        for i in range(self.stats()["entries"]):
+            b, n = C.c_int32(), C.c_int32()
+            check(lib().cev_prefix_store_entry(self.handle, i, C.byref(b), C.byref(n)))
+            out.append((b.value, n.value))
+        return out
 
 
 @dataclass

@@ -21,6 +21,7 @@ CEV_F32 = 0
 CEV_BF16 = 1
 CEV_MAX_SPANS = 4
 CEV_ATTN_SCRATCH_BYTES = 64 << 20
+CEV_LINEAR_WORKSPACE_BYTES = 32 << 20
 
 i32 = C.c_int32
 i64 = C.c_int64
@@ -99,6 +100,7 @@ SIGNATURES = {
     "cev_packed_attention_noalloc": (i32, [C.POINTER(AttnDesc), P, P, P, P, P, P, P, P, P, P]),
     "cev_qknorm_desc_init": (i32, [C.POINTER(QkNormDesc), i32, i32, i32, i32, i32, i32, i32, i32, C.c_float, i32]),
     "cev_qknorm_rope": (i32, [C.POINTER(QkNormDesc), P, P, P, P, P, P, P, P, P, P]),
+    "cev_qknorm_rope_kv": (i32, [C.POINTER(QkNormDesc), P, P, P, i64, i64, P, P, P, P, P, P, i32, P, P, P, i64, i64, P]),
     "cev_rope_table": (i32, [C.c_double, i32, i32, i32, P, P]),
     "cev_gdn_desc_init": (i32, [C.POINTER(GdnDesc), i32, i32, i32, i32, i32, i32, i32, i32, C.c_float]),
     "cev_gdn_workspace_size": (i32, [C.POINTER(GdnDesc), C.POINTER(C.c_size_t)]),
@@ -106,8 +108,21 @@ SIGNATURES = {
     "cev_rms_norm": (i32, [i32, i64, i32, P, i64, P, i64, P, i64, P, C.c_float, i32, P, i64, P]),
     "cev_swiglu": (i32, [i32, i64, i32, P, P, i64, P, i64, P]),
     "cev_debias_scores": (i32, [i32, i32, P, P, P, P, P, P, i32, P, P]),
+    "cev_blas_create": (i32, [C.POINTER(P)]),
+    "cev_blas_destroy": (i32, [P]),
+    "cev_linear": (i32, [P, i32, i32, i64, i64, i64, P, i64, P, i64, C.c_float, P, i64, P, C.c_size_t, P]),
+    "cev_gather_rows": (i32, [i32, i32, i64, i64, P, i64, i64, P, P, i64, P]),
     "cev_table_from_plans": (i32, [i32, Pi32, Pi32, Pi32, i32, Pi32, Pi32, PBlock, i32, Pi32, Pi32, i32, Pi32, Pi32]),
     "cev_table_from_rows": (i32, [i32, i32, i32, i32, Pi32, PBlock, i32]),
+    "cev_table_from_slots": (i32, [i32, Pi32, Pi32, Pi32, i32, Pi32, Pi32, Pi32, i32, PBlock, i32, Pi32, Pi32, Pi32, i32, Pi32, Pi32]),
+    "cev_prefix_store_create": (i32, [i32, i64, C.POINTER(P)]),
+    "cev_prefix_store_destroy": (i32, [P]),
+    "cev_prefix_store_get": (i32, [P, C.POINTER(C.c_uint32), i32, Pi32, Pi32]),
+    "cev_prefix_store_reserve": (i32, [P, i32, Pi32]),
+    "cev_prefix_store_put": (i32, [P, C.POINTER(C.c_uint32), i32, i32]),
+    "cev_prefix_store_release": (i32, [P, i32]),
+    "cev_prefix_store_stats": (i32, [P, Pi32, C.POINTER(i64), Pi32]),
+    "cev_prefix_store_entry": (i32, [P, i32, Pi32, Pi32]),
     "cev_table_from_segment_ids": (i32, [C.POINTER(C.c_uint32), i32, i32, PBlock, i32, Pi32]),
     "cev_table_to_dense_mask": (i32, [PBlock, i32, i32, i32, P]),
     "cev_table_from_dense_mask": (i32, [P, i32, i32, PBlock, i32, Pi32]),

@@ -11,7 +11,9 @@ are f32 (holding bf16-exact values for bf16 workloads).
       Hkv=8, d=128, positions restart at 32768.
   c4  Qwen3.5-style gated layer, bf16, bidirectional (d3): one 8192-token row,
       Hq=16, Hkv=4, d=256, rotary 64 of 256 dims (theta 1e7), weight 1 + w,
-      sigmoid output gate.
+      sigmoid output gate; read out at the last position through o_proj
+      (hidden 2048) and a random 255 x 2048 f32 readout matrix at
+      temperature 0.8 (d3's Kind::Matrix, hybrid.rs:657).
   c5a the gated-attention half of the hybrid pair: 32 rows right-padded to
       64 tokens continue a 4096-token prefix (Hq=16, Hkv=4, d=256).
   hbm the long-prefix short-suffix shape: c3 with 1 block x 16 tokens.
@@ -47,6 +49,7 @@ class AttnWorkload:
     eps: float = 1e-6
     lengths: Optional[List[int]] = None   # real tokens per row (padded rows)
     pos0: Optional[int] = None      # first suffix position (default: prefix)
+    readout: Optional[Tuple[int, int, float]] = None  # d3 readout: (hidden, codes, temperature)
     notes: str = ""
 
     @property
@@ -114,6 +117,15 @@ class AttnWorkload:
         wk = synth.tensor(self.seed, S_WK, (self.d,), self.bf16, scale=0.1, offset=off)
         return wq, wk
 
+    def readout_weights(self):
+        """d3 readout: o_proj (hidden, hq d) N(0, 0.02) in the model dtype
+        and the readout matrix (codes, hidden) N(0, 0.02) in f32 (load.rs
+        converts it to f32)."""
+        hidden, codes, _ = self.readout
+        wo = synth.tensor(self.seed, S_WO, (hidden, self.hq * self.d), self.bf16, scale=0.02)
+        wr = synth.tensor(self.seed, S_WR, (codes, hidden), False, scale=0.02)
+        return wo, wr
+
     def plans_items(self):
         """engine.rs packing: one plan whose whole prefix is cached, one
         question item per block."""
@@ -139,7 +151,15 @@ def hbm(blocks: int = 1) -> AttnWorkload:
 
 def c4() -> AttnWorkload:
     return AttnWorkload("c4", 4, True, 16, 4, 256, 0, [8192], 1e7, 64, causal=False, gated=True, plus_one=True,
-                        lengths=[8192], pos0=0, notes="Qwen3.5-style gated layer, bf16, bidirectional 8192-token row")
+                        lengths=[8192], pos0=0, readout=(2048, 255, 0.8),
+                        notes="Qwen3.5-style gated layer, bf16, bidirectional 8192-token row, d3 readout at the last position")
+
+
+def d3_f32() -> AttnWorkload:
+    """A small f32 case of c4's shape family for the d3 readout's f32 bar:
+    one 64-token bidirectional gated row, Hq=4, Hkv=2, d=128, hidden 256."""
+    return AttnWorkload("d3f32", 6, False, 4, 2, 128, 0, [64], 1e7, 32, causal=False, gated=True, plus_one=True, lengths=[64],
+                        pos0=0, readout=(256, 255, 0.8), notes="f32 gated bidirectional row with a d3 readout")
 
 
 def c5_attention() -> AttnWorkload:

@@ -5,7 +5,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import BlockTable, PackedAttention, Rotary, qknorm_rope
+from . import BlockTable, D3Readout, PackedAttention, Rotary, qknorm_rope
 from .configs import AttnWorkload
 
 
@@ -64,6 +64,13 @@ class AttentionLayer:
         self.table = default_table(w) if table is None else table
         self.attn = PackedAttention(self.q, self.k, self.table, k_cache=self.pk, s_cache=w.prefix, has_gate=w.gated, out=self.out,
                                     gate=self.gate, v_new=self.v, v_cache=self.pv)
+        # d3 workloads read the last position out through o_proj and the
+        # readout matrix (hybrid.rs:657)
+        self.readout = None
+        self.logits = None
+        if w.readout is not None:
+            wo, wr = w.readout_weights()
+            self.readout = D3Readout(wo, wr, w.readout[2], device, self.dtype)
 
     def qknorm(self):
         qknorm_rope(self.q_in, self.k_in, self.wq, self.wk, self.pos, self.rot, self.w.eps, plus_one=self.w.plus_one, q_out=self.q,
@@ -72,6 +79,15 @@ class AttentionLayer:
     def attend(self):
         return self.attn(self.q, self.k, self.v, self.pk, self.pv, self.gate, self.out)
 
+    def read_out(self):
+        """Logits (1, codes) f32 of the last position (hybrid.rs:634, :657)."""
+        w = self.w
+        self.logits = self.readout(self.out[w.t - 1: w.t].view(1, w.hq * w.d))
+        return self.logits
+
     def forward(self):
         self.qknorm()
-        return self.attend()
+        out = self.attend()
+        if self.readout is not None:
+            self.read_out()
+        return out

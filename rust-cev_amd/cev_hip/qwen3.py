@@ -1,26 +1,26 @@
 """A device-resident Qwen3 decoder stack around the packed attention path.
 
 The host mirror of Qwen3::prefill and Qwen3::forward_packed
-(crates/cev-model/src/qwen3.rs:346-401) with everything on the GPU:
-  - the projections are library GEMMs (torch.matmul -> hipBLASLt), q/k/v
-    fused into one and gate/up into another;
-  - K1 (cev_qknorm_rope) writes normalised, rotated q and k, and k lands
-    straight in this pass's slots of the layer's device K cache;
-  - K2 (cev_packed_attention) reads the cache as (past, new) through two
-    base pointers and the block table: no mask, no repeat_kv, no cat;
+(crates/cev-model/src/qwen3.rs:346-401) with everything on the GPU and every
+compute call through the C ABI (torch only holds device memory):
+  - embedding rows, the answer-row gather and the f32 conversion are
+    cev_gather_rows (qwen3.rs:288-293, :399-400);
+  - the projections are cev_linear (hipBLASLt GEMMs), q/k/v fused into one
+    and gate/up into another (qwen3.rs:175-178, :229-233);
+  - K1 (cev_qknorm_rope_kv) writes normalised, rotated q, and stores k and v
+    straight into their slots of the layer's device caches;
+  - K2 (cev_packed_attention) reads every key from those caches through the
+    slot-addressed block table: no mask, no repeat_kv, no cat;
   - the norms, residual adds and SwiGLU are cev_rms_norm / cev_swiglu.
-The per-layer K/V caches are preallocated (hkv, capacity, d) device tensors:
-a chunked prefill appends in place, and a packed pass's tail slots become
-part of the cached prefix without a copy (engine.rs:445-461 concatenates
-instead).
+Every layer owns one (hkv, capacity, d) K cache and one V cache with the
+same slot numbering; a cev_prefix_store (cev_hip.PrefixStore) decides which
+slots hold which cached prefix (cev_hip.engine.DeviceEngine).
 """
 from __future__ import annotations
 
-from typing import Optional
-
 import numpy as np
 
-from . import BlockTable, PackedAttention, Rotary, qknorm_rope, rms_norm, swiglu
+from . import (BlockTable, PackedAttention, Rotary, gather_rows, linear, qknorm_rope_kv, rms_norm, swiglu)
 
 
 class Qwen3Stack:
@@ -54,88 +54,91 @@ class Qwen3Stack:
             ))
         self.norm = dev(weights["norm"])
         self.capacity = capacity
-        self.rot = Rotary(w.theta, w.d, capacity, self.dtype, device)
-        self.cached = 0  # tokens in the K/V caches
+        self.rot = Rotary(w.theta, w.d, capacity + w.questions * w.q_len + 1, self.dtype, device)
         self.max_splits = max_splits  # split policy of the attention plans (0: the planner's)
+        self._heads = {}
 
-    def _run(self, tokens, pos, table: BlockTable, keep: bool) -> "torch.Tensor":
-        """All layers over the packed new tokens; their K/V land in cache
-        slots [cached, cached + t).  Returns the last residual stream (t, H)."""
+    def run(self, tokens, pos, slots, table: BlockTable):
+        """All layers over the packed new tokens (Qwen3::forward_packed's
+        layer loop, qwen3.rs:389-398); token i's K/V land in cache slot
+        slots[i] of every layer.  The table is slot-addressed (s_cache =
+        capacity).  Returns (x, h): the residual stream before the last
+        layer's MLP residual add and that MLP output (t, H)."""
         import torch
         w = self.w
-        t, s0 = len(tokens), self.cached
-        if table.t != t or table.s_cache != s0:
-            raise ValueError(f"table is for t={table.t}, s_cache={table.s_cache}; pass has t={t}, cached={s0}")
-        if s0 + t > self.capacity:
-            raise ValueError(f"cache capacity {self.capacity} < {s0 + t} tokens")
+        t = len(tokens)
+        if table.t != t or table.s_cache != self.capacity:
+            raise ValueError(f"table is for t={table.t}, s_cache={table.s_cache}; pass has t={t}, capacity={self.capacity}")
         H, hq, hkv, d = w.hidden, w.hq, w.hkv, w.d
-        ids = torch.as_tensor(np.asarray(tokens, np.int64), device=self.device)
-        pos_d = torch.as_tensor(np.asarray(pos, np.int32), device=self.device)
-        x = self.embed.index_select(0, ids)
+        i32 = lambda a: torch.as_tensor(np.ascontiguousarray(a, np.int32), device=self.device)  # noqa: E731
+        ids, pos_d, slots_d = i32(tokens), i32(pos), i32(slots)
+        x = gather_rows(self.embed, ids)
         y = torch.empty_like(x)
         q = torch.empty((t, hq, d), dtype=self.dtype, device=self.device)
         o = torch.empty((t, hq, d), dtype=self.dtype, device=self.device)
         act = torch.empty((t, w.inter), dtype=self.dtype, device=self.device)
-        attn: Optional[PackedAttention] = None
+        qkv = torch.empty((t, (hq + 2 * hkv) * d), dtype=self.dtype, device=self.device)
+        gu = torch.empty((t, 2 * w.inter), dtype=self.dtype, device=self.device)
+        h = torch.empty_like(x)
+        L0 = self.layers[0]
+        # every key is a cache slot: the "new" K/V views are never read
+        attn = PackedAttention(q, L0["k"].transpose(0, 1), table, k_cache=L0["k"], s_cache=self.capacity, out=o,
+                               v_new=L0["v"].transpose(0, 1), v_cache=L0["v"], max_splits=self.max_splits)
         for i, L in enumerate(self.layers):
             # ln1: the first layer's input is the embedding; later ones come
             # fused with the previous layer's MLP residual add below
             if i == 0:
                 rms_norm(x, L["ln1"], w.eps, y=y)
-            qkv = torch.matmul(y, L["wqkv"].t())
+            linear(y, L["wqkv"], out=qkv)
             q_in = qkv[:, : hq * d].view(t, hq, d)
             k_in = qkv[:, hq * d: (hq + hkv) * d].view(t, hkv, d)
             v_in = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
-            k_new = L["k"][:, s0: s0 + t].transpose(0, 1)  # (t, hkv, d) view of the cache slots
-            v_new = L["v"][:, s0: s0 + t].transpose(0, 1)
-            qknorm_rope(q_in, k_in, L["q_norm"], L["k_norm"], pos_d, self.rot, w.eps, q_out=q, k_out=k_new)
-            v_new.copy_(v_in)
-            kc, vc = L["k"][:, :s0], L["v"][:, :s0]
-            if attn is None:
-                attn = PackedAttention(q, k_new, table, k_cache=kc if s0 else None, s_cache=s0, out=o, v_new=v_new,
-                                       v_cache=vc if s0 else None, max_splits=self.max_splits)
-            attn(q, k_new, v_new, kc if s0 else None, vc if s0 else None, None, o)
-            h = torch.matmul(o.view(t, hq * d), L["wo"].t())
+            kt, vt = L["k"].transpose(0, 1), L["v"].transpose(0, 1)  # (capacity, hkv, d) views
+            qknorm_rope_kv(q_in, k_in, v_in, L["q_norm"], L["k_norm"], pos_d, self.rot, w.eps, q, kt, vt, slots=slots_d,
+                           n_slots=self.capacity)
+            attn(q, kt, vt, L["k"], L["v"], None, o)
+            linear(o.view(t, hq * d), L["wo"], out=h)
             rms_norm(x, L["ln2"], w.eps, h=h, x_out=x, y=y)  # x += h; y = ln2(x)
-            gu = torch.matmul(y, L["wgu"].t())
+            linear(y, L["wgu"], out=gu)
             swiglu(gu[:, : w.inter], gu[:, w.inter:], out=act)
-            h = torch.matmul(act, L["wdown"].t())
-            nxt = self.layers[i + 1]["ln1"] if i + 1 < len(self.layers) else None
-            if nxt is not None:
-                rms_norm(x, nxt, w.eps, h=h, x_out=x, y=y)  # x += h; y = next ln1(x)
-            else:
-                x.add_(h)
-        if keep:
-            self.cached = s0 + t
-        return x
+            linear(act, L["wdown"], out=h)
+            if i + 1 < len(self.layers):
+                rms_norm(x, self.layers[i + 1]["ln1"], w.eps, h=h, x_out=x, y=y)  # x += h; y = next ln1(x)
+        return x, h
 
-    def prefill(self, tokens, chunk: int):
-        """Qwen3::prefill (qwen3.rs:346-362): chunks seeing the cache and
-        themselves causally, appended to the cache in place."""
-        for c0 in range(0, len(tokens), max(1, chunk)):
-            part = tokens[c0: c0 + chunk]
-            n = len(part)
-            table = BlockTable.from_segment_ids(np.zeros(n, np.uint32), past=self.cached)
-            self._run(part, np.arange(self.cached, self.cached + n, dtype=np.int32), table, keep=True)
-
-    def forward_packed(self, tokens, pos, table: BlockTable, gather, keep_tokens: int = 0):
-        """Qwen3::forward_packed (qwen3.rs:364-401): the final-normed hidden
-        state (f32) at the gather rows.  The first keep_tokens new tokens
-        (a plan's tail) stay in the cache; later slots are reused."""
+    def hidden(self, xh, gather):
+        """The last residual add and the final norm at the gather rows, as
+        f32 (qwen3.rs:397-400): rows are independent, so the add runs on the
+        gathered rows only."""
         import torch
-        x = self._run(tokens, pos, table, keep=False)
-        g = torch.as_tensor(np.asarray(gather, np.int64), device=self.device)
-        xg = x.index_select(0, g)
-        hidden = rms_norm(xg, self.norm, self.w.eps).to(torch.float32)
-        self.cached += keep_tokens
-        return hidden
+        x, h = xh
+        g = torch.as_tensor(np.ascontiguousarray(gather, np.int32), device=self.device)
+        xg, hg = gather_rows(x, g), gather_rows(h, g)
+        y = rms_norm(xg, self.norm, self.w.eps, h=hg, x_out=xg)
+        return gather_rows(y, out_dtype=torch.float32)
+
+    def prefill(self, begin: int, tokens, chunk: int):
+        """Qwen3::prefill (qwen3.rs:346-362) into slots begin .. begin +
+        len(tokens): 512-token chunks that see the slots before them and
+        themselves causally (segment_mask, qwen3.rs:157-169)."""
+        n = len(tokens)
+        for c0 in range(0, n, max(1, chunk)):
+            part = tokens[c0: c0 + chunk]
+            tab, pos, slots, _ = BlockTable.from_slots([(begin, c0 + len(part), c0)], [], self.capacity)
+            self.run(part, pos, slots, tab)
+
+    def code_head(self, code_ids):
+        """The code rows of the tied head as f32 (engine.rs:155)."""
+        import torch
+        key = tuple(int(c) for c in code_ids)
+        if key not in self._heads:
+            ids = torch.as_tensor(np.asarray(key, np.int32), device=self.device)
+            self._heads[key] = gather_rows(self.embed, ids, out_dtype=torch.float32)
+        return self._heads[key]
 
     def code_logits(self, hidden, code_ids):
-        """hidden . code_head^T with code_head = the tied head's rows for the
-        code tokens, in f32 (engine.rs:155, :463)."""
-        import torch
-        head = self.embed.index_select(0, torch.as_tensor(np.asarray(code_ids, np.int64), device=self.device)).to(torch.float32)
-        return torch.matmul(hidden, head.t())
+        """hidden . code_head^T in f32 (engine.rs:463)."""
+        return linear(hidden, self.code_head(code_ids))
 
 
 def softmax64(z) -> np.ndarray:

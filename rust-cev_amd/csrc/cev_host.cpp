@@ -512,6 +512,105 @@ extern "C" int32_t cev_table_from_plans(int32_t n_plans, const int32_t* past_len
   return CEV_OK;
 }
 
+extern "C" int32_t cev_table_from_slots(int32_t n_plans, const int32_t* kv_begin, const int32_t* prefix_len, const int32_t* tail_start,
+                                        int32_t n_items, const int32_t* item_plan, const int32_t* item_len, const int32_t* item_slot,
+                                        int32_t capacity, cev_block* blocks, int32_t max_blocks, int32_t* n_out_blocks, int32_t* pos,
+                                        int32_t* slots, int32_t max_tokens, int32_t* n_tokens, int32_t* gather) {
+  CEV_CHECK_ARG(n_plans >= 0 && n_items >= 0 && capacity >= 0, "negative plan count, item count or capacity");
+  CEV_CHECK_ARG(n_plans == 0 || (kv_begin && prefix_len && tail_start), "null plan arrays");
+  CEV_CHECK_ARG(n_items == 0 || (item_plan && item_len && item_slot), "null item arrays");
+  // Slot ranges this pass reads (computed prefixes) and writes (tails and
+  // questions): inside the cache, and no written range may overlap another
+  // range of the pass.
+  struct Iv {
+    int64_t b, e;
+    bool write;
+  };
+  std::vector<Iv> iv;
+  int64_t n = 0;
+  int32_t nb = 0;
+  for (int32_t p = 0; p < n_plans; ++p) {
+    CEV_CHECK_ARG(prefix_len[p] >= 0 && tail_start[p] >= 0 && tail_start[p] <= prefix_len[p], "plan %d: tail_start %d outside [0, %d]", p,
+                  tail_start[p], prefix_len[p]);
+    CEV_CHECK_ARG(kv_begin[p] >= 0 && (int64_t)kv_begin[p] + prefix_len[p] <= capacity, "plan %d: slots [%d, %lld) outside [0, %d)", p,
+                  kv_begin[p], (long long)kv_begin[p] + prefix_len[p], capacity);
+    if (tail_start[p] > 0) iv.push_back({kv_begin[p], (int64_t)kv_begin[p] + tail_start[p], false});
+    if (prefix_len[p] > tail_start[p]) {
+      iv.push_back({(int64_t)kv_begin[p] + tail_start[p], (int64_t)kv_begin[p] + prefix_len[p], true});
+      n += prefix_len[p] - tail_start[p];
+      nb++;
+    }
+  }
+  for (int32_t k = 0; k < n_items; ++k) {
+    CEV_CHECK_ARG(item_plan[k] >= 0 && item_plan[k] < n_plans, "item %d: plan %d outside [0, %d)", k, item_plan[k], n_plans);
+    CEV_CHECK_ARG(item_len[k] >= 1, "item %d: empty question", k);
+    CEV_CHECK_ARG(item_slot[k] >= 0 && (int64_t)item_slot[k] + item_len[k] <= capacity, "item %d: slots [%d, %lld) outside [0, %d)", k,
+                  item_slot[k], (long long)item_slot[k] + item_len[k], capacity);
+    iv.push_back({item_slot[k], (int64_t)item_slot[k] + item_len[k], true});
+    n += item_len[k];
+    nb++;
+  }
+  std::sort(iv.begin(), iv.end(), [](const Iv& a, const Iv& b) { return a.b < b.b; });
+  for (size_t i = 1; i < iv.size(); ++i)
+    for (size_t j = i; j-- > 0;) {
+      if (iv[j].e <= iv[i].b) break;
+      if (iv[i].write || iv[j].write)
+        return cev_fail(CEV_ERR_INVALID, "slots [%lld, %lld) written by this pass overlap [%lld, %lld)", (long long)iv[i].b,
+                        (long long)iv[i].e, (long long)iv[j].b, (long long)iv[j].e);
+    }
+  CEV_CHECK_ARG((int64_t)capacity + n <= INT32_MAX, "pass too large");
+  if (n_tokens) *n_tokens = (int32_t)n;
+  if (n_out_blocks) *n_out_blocks = nb;
+  if (!blocks && !pos && !slots && !gather) return CEV_OK;
+  if (blocks && max_blocks < nb) return cev_fail(CEV_ERR_SPACE, "table needs %d blocks, buffer has %d", nb, max_blocks);
+  if ((pos || slots) && max_tokens < n) return cev_fail(CEV_ERR_SPACE, "pass has %lld tokens, buffer has %d", (long long)n, max_tokens);
+  // Tokens: tails first in plan order, then questions (engine.rs:393-416).
+  int32_t bi = 0;
+  int64_t tok = 0;
+  for (int32_t p = 0; p < n_plans; ++p) {
+    const int32_t tl = prefix_len[p] - tail_start[p];
+    if (tl == 0) continue;
+    if (blocks) {
+      cev_block& b = blocks[bi];
+      memset(&b, 0, sizeof b);
+      b.q_begin = (int32_t)tok;
+      b.q_len = tl;
+      b.valid_len = tl;
+      b.causal = 1;  // the tail sees its plan's past, and itself causally (engine.rs:429)
+      b.local_begin = kv_begin[p] + tail_start[p];
+      if (tail_start[p] > 0) b.spans[b.n_spans++] = {kv_begin[p], tail_start[p]};
+    }
+    for (int32_t j = 0; j < tl; ++j) {
+      if (pos) pos[tok + j] = tail_start[p] + j;
+      if (slots) slots[tok + j] = kv_begin[p] + tail_start[p] + j;
+    }
+    tok += tl;
+    bi++;
+  }
+  for (int32_t k = 0; k < n_items; ++k) {
+    const int32_t p = item_plan[k];
+    if (blocks) {
+      cev_block& b = blocks[bi];
+      memset(&b, 0, sizeof b);
+      b.q_begin = (int32_t)tok;
+      b.q_len = item_len[k];
+      b.valid_len = item_len[k];
+      b.causal = 1;
+      b.local_begin = item_slot[k];
+      // the plan's past and tail are one contiguous run of slots
+      if (prefix_len[p] > 0) b.spans[b.n_spans++] = {kv_begin[p], prefix_len[p]};
+    }
+    for (int32_t j = 0; j < item_len[k]; ++j) {
+      if (pos) pos[tok + j] = prefix_len[p] + j;  // restart (engine.rs:411)
+      if (slots) slots[tok + j] = item_slot[k] + j;
+    }
+    tok += item_len[k];
+    if (gather) gather[k] = (int32_t)tok - 1;
+    bi++;
+  }
+  return CEV_OK;
+}
+
 extern "C" int32_t cev_table_from_rows(int32_t b, int32_t t, int32_t past, int32_t causal, const int32_t* lengths, cev_block* blocks,
                                        int32_t max_blocks) {
   CEV_CHECK_ARG(b >= 0 && t >= 1 && past >= 0, "bad row batch (b %d, t %d, past %d)", b, t, past);

@@ -28,6 +28,8 @@
 //   qknorm_rope_kernel (any other shape): a wave normalises 8 vectors at a
 //     time; lanes load coalesced, the squares go through LDS and lanes 0..7
 //     each sum one vector.
+#include <algorithm>
+
 #include "cev_device.h"
 #include "cev_internal.h"
 
@@ -46,7 +48,43 @@ struct QkArgs {
   int64_t qi_st, qi_sh, ki_st, ki_sh, qo_st, qo_sh, ko_st, ko_sh;
   int32_t t, hq, hkv, rot, n_pos, plus_one;
   float eps;
+  // Optional: token i's k (and v) rows go to row slots[i] of k_out (v_out)
+  // instead of row i; v rows are copied unchanged by the workgroups from
+  // qk_blocks on.
+  const int32_t* slots;
+  int32_t n_slots;
+  int32_t qk_blocks;
+  const void* v_in;
+  void* v_out;
+  int64_t vi_st, vi_sh, vo_st, vo_sh;
 };
+
+// Output row of token tk's k and v: slots[tk] when the caller maps tokens to
+// cache slots, else tk; a slot outside [0, n_slots) stores nothing.
+__device__ __forceinline__ int64_t kv_row(const QkArgs& a, int tk) {
+  if (!a.slots) return tk;
+  const int s = a.slots[tk];
+  return (s >= 0 && s < a.n_slots) ? (int64_t)s : -1;
+}
+
+// The v part of a call (workgroups from a.qk_blocks on): every v row copied
+// to its output row in 16-byte chunks, grid-strided.
+template <typename T, int D>
+__device__ void copy_v_rows(const QkArgs& a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int NCH = D / VEC;
+  const int64_t total = (int64_t)a.t * a.hkv * NCH;
+  const int64_t stride = (int64_t)(gridDim.x - a.qk_blocks) * blockDim.x;
+  for (int64_t i = (int64_t)(blockIdx.x - a.qk_blocks) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t vr = i / NCH;
+    const int ch = (int)(i % NCH);
+    const int tk = (int)(vr / a.hkv), h = (int)(vr % a.hkv);
+    const int64_t r = kv_row(a, tk);
+    if (r < 0) continue;
+    const uint4 v = *(const uint4*)((const T*)a.v_in + tk * a.vi_st + h * a.vi_sh + ch * VEC);
+    *(uint4*)((T*)a.v_out + r * a.vo_st + h * a.vo_sh + ch * VEC) = v;
+  }
+}
 
 constexpr int VPW = 8;    // vectors per wave
 constexpr int WAVES = 4;  // waves per workgroup
@@ -79,6 +117,10 @@ __global__ __launch_bounds__(WAVES * 64) void qknorm_rope_kernel(QkArgs a) {
   constexpr int EPL = D / 64;  // elements per lane per vector
   __shared__ float buf[WAVES][VPW][D];
   __shared__ float msh[WAVES][VPW];
+  if ((int)blockIdx.x >= a.qk_blocks) {
+    copy_v_rows<T, D>(a);
+    return;
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t nq = (int64_t)a.t * a.hq;
   const int64_t total = nq + (int64_t)a.t * a.hkv;
@@ -107,7 +149,8 @@ __global__ __launch_bounds__(WAVES * 64) void qknorm_rope_kernel(QkArgs a) {
       const int64_t vk = v - nq;
       const int tk = (int)(vk / a.hkv), h = (int)(vk % a.hkv);
       src[j] = (const T*)a.k_in + tk * a.ki_st + h * a.ki_sh;
-      dst[j] = (T*)a.k_out + tk * a.ko_st + h * a.ko_sh;
+      const int64_t r = kv_row(a, tk);
+      dst[j] = r >= 0 ? (T*)a.k_out + r * a.ko_st + h * a.ko_sh : nullptr;
       wgt[j] = (const T*)a.w_k;
       tok[j] = tk;
     }
@@ -228,6 +271,10 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<
   constexpr int NR = NC / 8;  // staging rounds
   static_assert(NC % 8 == 0, "whole staging rounds");
   __shared__ __align__(16) char stage[TPB / 64][64 * kStageRow];
+  if ((int)blockIdx.x >= a.qk_blocks) {
+    copy_v_rows<T, D>(a);
+    return;
+  }
   for (int i = threadIdx.x; i < 2 * D; i += TPB) {
     const T* wsrc = i < D ? (const T*)a.w_q : (const T*)a.w_k;
     const bool have = i < D ? a.hq > 0 : a.hkv > 0;
@@ -264,7 +311,8 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<
     tk = (int)(vk / a.hkv);
     const int h = (int)(vk % a.hkv);
     src = (const T*)a.k_in + tk * a.ki_st + h * a.ki_sh;
-    dst = (T*)a.k_out + tk * a.ko_st + h * a.ko_sh;
+    const int64_t r = kv_row(a, tk);
+    dst = r >= 0 ? (T*)a.k_out + r * a.ko_st + h * a.ko_sh : nullptr;
   }
   const float* wl = weff[is_q ? 0 : 1];
   const int lane = threadIdx.x & 63;
@@ -407,7 +455,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<
     // values of every pair would stay live at once and spill).
 #pragma unroll
     for (int k = 0; k < NC; ++k) asm volatile("" : "+v"(c[k]));
-    const uint64_t dp = valid ? (uint64_t)dst : 0;
+    const uint64_t dp = (valid && dst) ? (uint64_t)dst : 0;
     const int sub = lane >> 3, kc = lane & 7;
     gptr<u32x4> vdst[8];
 #pragma unroll
@@ -424,7 +472,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<
       }
       wave_lds_sync();
     }
-  } else if (valid) {
+  } else if (valid && dst) {
     // Rare (a wave with a tiny, huge or non-finite element): IEEE division,
     // one chunk or rotary pair at a time, re-read from the input (each
     // chunk is read before its own store, so q_out may alias q_in).
@@ -481,6 +529,10 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
   static_assert(E % VEC == 0 && (ROT == D || ROT == D / 4), "whole chunks; full or quarter rotary");
   auto rnd = [](float x) { return BF ? bf16_round(x) : x; };
   __shared__ __align__(16) float weff[2][D];
+  if ((int)blockIdx.x >= a.qk_blocks) {
+    copy_v_rows<T, D>(a);
+    return;
+  }
   for (int i = threadIdx.x; i < 2 * D; i += kQuadThreads) {
     const T* wsrc = i < D ? (const T*)a.w_q : (const T*)a.w_k;
     const bool have = i < D ? a.hq > 0 : a.hkv > 0;
@@ -518,7 +570,8 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
     tk = (int)(vk / a.hkv);
     const int h = (int)(vk % a.hkv);
     src = (const T*)a.k_in + tk * a.ki_st + h * a.ki_sh;
-    dst = (T*)a.k_out + tk * a.ko_st + h * a.ko_sh;
+    const int64_t r = kv_row(a, tk);
+    dst = r >= 0 ? (T*)a.k_out + r * a.ko_st + h * a.ko_sh : nullptr;
   }
   const float* wl = weff[is_q ? 0 : 1] + j * E;
   u32x4 c[NCL];
@@ -639,15 +692,27 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
     body(std::true_type{});
   else
     body(std::false_type{});
-  if (valid) {
+  if (valid && dst) {
 #pragma unroll
     for (int k = 0; k < NCL; ++k) *(u32x4*)(dst + j * E + k * VEC) = c[k];
   }
 }
 
+// Workgroups that copy v after the q/k ones: one 16-byte chunk per thread,
+// at most kVBlocks workgroups striding over the rest.
+constexpr int64_t kVBlocks = 2048;
 template <typename T>
-int32_t launch_quad(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
-  const int64_t grid = (4 * vecs + kQuadThreads - 1) / kQuadThreads;
+int64_t v_blocks(const QkArgs& a, int d, int tpb) {
+  if (!a.v_in) return 0;
+  const int64_t chunks = (int64_t)a.t * a.hkv * (d / (16 / (int)sizeof(T)));
+  return std::min<int64_t>(kVBlocks, (chunks + tpb - 1) / tpb);
+}
+
+template <typename T>
+int32_t launch_quad(QkArgs a, int d, int64_t vecs, hipStream_t s) {
+  const int64_t qk = (4 * vecs + kQuadThreads - 1) / kQuadThreads;
+  a.qk_blocks = (int32_t)qk;
+  const int64_t grid = qk + v_blocks<T>(a, d, kQuadThreads);
   const dim3 g((unsigned)grid), b(kQuadThreads);
   if (d == 128 && a.rot == 128)
     hipLaunchKernelGGL((qknorm_rope_quad_kernel<T, 128, 128>), g, b, 0, s, a);
@@ -667,9 +732,11 @@ int32_t launch_quad(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
 }
 
 template <typename T, int TPB>
-int32_t launch_lane(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
-  const int64_t grid = (vecs + TPB - 1) / TPB;
-  if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm grid too large");
+int32_t launch_lane(QkArgs a, int d, int64_t vecs, hipStream_t s) {
+  const int64_t qk = (vecs + TPB - 1) / TPB;
+  if (qk > INT32_MAX / 2) return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm grid too large");
+  a.qk_blocks = (int32_t)qk;
+  const int64_t grid = qk + v_blocks<T>(a, d, TPB);
   const dim3 g((unsigned)grid), b(TPB);
   if (d == 128 && a.rot == 128)
     hipLaunchKernelGGL((qknorm_rope_lane_kernel<T, 128, 128, TPB>), g, b, 0, s, a);
@@ -689,7 +756,7 @@ int32_t launch_lane(const QkArgs& a, int d, int64_t vecs, hipStream_t s) {
 }
 
 template <typename T>
-int32_t launch_qk(const QkArgs& a, int d, hipStream_t s) {
+int32_t launch_qk(QkArgs a, int d, hipStream_t s) {
   const int64_t vecs = (int64_t)a.t * (a.hq + a.hkv);
   if (vecs == 0) return CEV_OK;
   if (lane_kernel_fits<T>(a, d)) {
@@ -700,8 +767,10 @@ int32_t launch_qk(const QkArgs& a, int d, hipStream_t s) {
     return launch_lane<T, kLaneThreads>(a, d, vecs, s);
   }
   const int64_t per_wg = (int64_t)WAVES * VPW;
-  const int64_t grid = (vecs + per_wg - 1) / per_wg;
-  if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm grid too large");
+  const int64_t qk = (vecs + per_wg - 1) / per_wg;
+  if (qk > INT32_MAX / 2) return cev_fail(CEV_ERR_UNSUPPORTED, "qknorm grid too large");
+  a.qk_blocks = (int32_t)qk;
+  const int64_t grid = qk + v_blocks<T>(a, d, WAVES * 64);
   if (d == 128)
     hipLaunchKernelGGL((qknorm_rope_kernel<T, 128>), dim3((unsigned)grid), dim3(WAVES * 64), 0, s, a);
   else
@@ -713,8 +782,11 @@ int32_t launch_qk(const QkArgs& a, int d, hipStream_t s) {
 
 }  // namespace
 
-extern "C" int32_t cev_qknorm_rope(const cev_qknorm_desc* d, const void* q_in, const void* k_in, const void* w_q, const void* w_k,
-                                   const int32_t* pos, const void* cos_t, const void* sin_t, void* q_out, void* k_out, cev_stream stream) {
+namespace {
+
+int32_t qknorm_rope_impl(const cev_qknorm_desc* d, const void* q_in, const void* k_in, const void* v_in, int64_t vi_st, int64_t vi_sh,
+                         const void* w_q, const void* w_k, const int32_t* pos, const void* cos_t, const void* sin_t, const int32_t* slots,
+                         int32_t n_slots, void* q_out, void* k_out, void* v_out, int64_t vo_st, int64_t vo_sh, cev_stream stream) {
   CEV_CHECK_ARG(d != nullptr, "cev_qknorm_rope: null descriptor");
   if (d->dtype != CEV_F32 && d->dtype != CEV_BF16) return cev_fail(CEV_ERR_UNSUPPORTED, "cev_qknorm_rope: dtype %d", d->dtype);
   if (d->head_dim != 128 && d->head_dim != 256) return cev_fail(CEV_ERR_UNSUPPORTED, "cev_qknorm_rope: head_dim %d", d->head_dim);
@@ -723,11 +795,19 @@ extern "C" int32_t cev_qknorm_rope(const cev_qknorm_desc* d, const void* q_in, c
                 d->rotary_dim);
   CEV_CHECK_ARG(d->n_pos >= 1, "cev_qknorm_rope: empty cos/sin table");
   CEV_CHECK_ARG(d->eps >= 0.0f, "cev_qknorm_rope: negative eps");
+  CEV_CHECK_ARG(!slots || n_slots >= 0, "cev_qknorm_rope: negative slot count");
   if (d->t == 0 || d->n_q_heads + d->n_kv_heads == 0) return CEV_OK;
   CEV_CHECK_ARG(pos && cos_t && sin_t, "cev_qknorm_rope: null pos or table");
   CEV_CHECK_ARG(d->n_q_heads == 0 || (q_in && q_out && w_q), "cev_qknorm_rope: null q buffers");
   CEV_CHECK_ARG(d->n_kv_heads == 0 || (k_in && k_out && w_k), "cev_qknorm_rope: null k buffers");
-  QkArgs a;
+  if (v_in || v_out) {
+    CEV_CHECK_ARG(v_in && v_out && d->n_kv_heads > 0, "cev_qknorm_rope_kv: v_in and v_out go together, with kv heads");
+    const int64_t vec = d->dtype == CEV_BF16 ? 8 : 4;
+    CEV_CHECK_ARG(((uintptr_t)v_in & 15) == 0 && ((uintptr_t)v_out & 15) == 0 && vi_st % vec == 0 && vi_sh % vec == 0 &&
+                      vo_st % vec == 0 && vo_sh % vec == 0 && vi_st >= 0 && vi_sh >= 0 && vo_st >= 0 && vo_sh >= 0,
+                  "cev_qknorm_rope_kv: v rows must be 16-byte aligned");
+  }
+  QkArgs a{};
   a.q_in = q_in;
   a.k_in = k_in;
   a.w_q = w_q;
@@ -752,7 +832,31 @@ extern "C" int32_t cev_qknorm_rope(const cev_qknorm_desc* d, const void* q_in, c
   a.n_pos = d->n_pos;
   a.plus_one = d->weight_plus_one;
   a.eps = d->eps;
+  a.slots = slots;
+  a.n_slots = n_slots;
+  a.qk_blocks = INT32_MAX;
+  a.v_in = v_in;
+  a.v_out = v_out;
+  a.vi_st = vi_st;
+  a.vi_sh = vi_sh;
+  a.vo_st = vo_st;
+  a.vo_sh = vo_sh;
   hipStream_t s = (hipStream_t)stream;
   if (d->dtype == CEV_BF16) return launch_qk<uint16_t>(a, d->head_dim, s);
   return launch_qk<float>(a, d->head_dim, s);
+}
+
+}  // namespace
+
+extern "C" int32_t cev_qknorm_rope(const cev_qknorm_desc* d, const void* q_in, const void* k_in, const void* w_q, const void* w_k,
+                                   const int32_t* pos, const void* cos_t, const void* sin_t, void* q_out, void* k_out, cev_stream stream) {
+  return qknorm_rope_impl(d, q_in, k_in, nullptr, 0, 0, w_q, w_k, pos, cos_t, sin_t, nullptr, 0, q_out, k_out, nullptr, 0, 0, stream);
+}
+
+extern "C" int32_t cev_qknorm_rope_kv(const cev_qknorm_desc* d, const void* q_in, const void* k_in, const void* v_in, int64_t vi_stride_t,
+                                      int64_t vi_stride_h, const void* w_q, const void* w_k, const int32_t* pos, const void* cos_t,
+                                      const void* sin_t, const int32_t* slots, int32_t n_slots, void* q_out, void* k_out, void* v_out,
+                                      int64_t vo_stride_t, int64_t vo_stride_h, cev_stream stream) {
+  return qknorm_rope_impl(d, q_in, k_in, v_in, vi_stride_t, vi_stride_h, w_q, w_k, pos, cos_t, sin_t, slots, n_slots, q_out, k_out, v_out,
+                          vo_stride_t, vo_stride_h, stream);
 }

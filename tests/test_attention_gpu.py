@@ -111,6 +111,74 @@ def test_c4_bidirectional_gated_sampled_rows(gpu, orc):
         _check_blocks(gl, ol, [0], BF16_TOL, rows=(r0, 32))
 
 
+def _d3_check(gpu, orc, w, tol):
+    """GPU: K1 + K2 over the whole row, then o_proj of the last position and
+    the readout (D3Readout through cev_linear / cev_gather_rows).  Oracle:
+    the same chain from the same inputs (attention of the last row by the
+    candle-op restatement, its gate, oracle.readout.d3_readout)."""
+    import torch
+    from oracle.readout import d3_readout
+    gl = GpuLayer(w, gpu)
+    ol = OracleLayer(orc, w, gl.np_inputs)
+    gl.forward()
+    torch.cuda.synchronize()
+    got = to_np(gl.logits)[0]
+    r = w.t - 1
+    o_last = ol.block(0, rows=(r, 1))[r].reshape(1, -1)
+    wo, wr = w.readout_weights()
+    want = d3_readout(o_last, wo, wr, w.readout[2], w.bf16)[0]
+    err = float(np.abs(got - want).max())
+    # the readout arithmetic alone, on the GPU's own attention row
+    own = d3_readout(to_np(gl.out)[r].reshape(1, -1), wo, wr, w.readout[2], w.bf16)[0]
+    err_own = float(np.abs(got - own).max())
+    scale = float(np.abs(want).max())
+    _say(f"{w.name} d3 readout: {got.size} logits, max|logit| {scale:.3g}, max|d| end to end {err:.3g}, "
+         f"readout alone {err_own:.3g}")
+    assert got.shape == (w.readout[1],) and np.isfinite(got).all()
+    assert err <= tol and err_own <= tol
+    return err
+
+
+def test_c4_d3_readout_full_row(gpu, orc):
+    """Config 4's observable: the 255 d3 logits at the last position of the
+    full 8192-token bidirectional gated row (hybrid.rs:657), bf16 bar."""
+    _d3_check(gpu, orc, configs.c4(), BF16_TOL)
+
+
+def test_d3_readout_f32_small(gpu, orc):
+    _d3_check(gpu, orc, configs.d3_f32(), F32_TOL)
+
+
+def test_linear_shapes_against_numpy(gpu, orc):
+    """cev_linear on both paths (own kernel for m <= 8, hipBLASLt above) and
+    both dtypes, with strided rows, against f64 products rounded once."""
+    import torch
+    from oracle.readout import linear as ref_linear
+    rng = np.random.default_rng(3)
+    for bf, m, n, k, out32 in ((True, 1, 2048, 4096, False), (True, 5, 300, 264, True), (False, 1, 255, 2048, True),
+                               (False, 8, 64, 512, True), (True, 96, 512, 1024, False), (False, 64, 8, 2048, True),
+                               (True, 3584, 4096, 2048, False)):
+        x = rng.standard_normal((m, k + 8)).astype(np.float32)[:, :k]
+        wt = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+        if bf:
+            x, wt = orc.round_bf16(x), orc.round_bf16(wt)
+        xd = to_dev(np.ascontiguousarray(np.pad(x, ((0, 0), (0, 8)))), bf, gpu)[:, :k]
+        wd = to_dev(wt, bf, gpu)
+        got = to_np(cev_hip.linear(xd, wd, alpha=0.5, out_dtype=torch.float32 if out32 else None))
+        want = ref_linear(x, wt, bf and not out32) * np.float32(0.5)
+        if bf and not out32:
+            want = orc.round_bf16(ref_linear(x, wt, False) * np.float32(0.5))
+        err = float(np.abs(got - want).max() / max(1e-30, np.abs(want).max()))
+        _say(f"linear bf16={bf} m={m} n={n} k={k} f32 out={out32}: max rel err {err:.3g}")
+        assert err <= (1e-2 if bf and not out32 else 1e-5)
+    # gather with conversion and an out-of-range id
+    tab = torch.randn(10, 16, device=gpu).to(torch.bfloat16)
+    ids = torch.tensor([3, 0, 9, 10], dtype=torch.int32, device=gpu)
+    g = to_np(cev_hip.gather_rows(tab, ids, out_dtype=torch.float32))
+    ref = to_np(tab)
+    assert np.array_equal(g[:3], ref[[3, 0, 9]]) and np.isnan(g[3]).all()
+
+
 def test_c5_gated_rows_continue_prefix(gpu, orc):
     w = configs.c5_attention()
     _say(f"test c5a: rows={len(w.blocks)} x {w.blocks[0]} P={w.prefix}")

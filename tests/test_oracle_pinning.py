@@ -561,3 +561,87 @@ def test_debias_calibration_against_itself_is_zero():
     logits = logits + rng.standard_normal(logits.shape).astype(np.float32)  # not invariant any more
     got = debias_scores(logits, order, begin, length, ks, calib=logits)
     assert np.array_equal(got, np.zeros_like(got))
+
+
+# ---------------------------------------------------------------------------
+# d3 readout (oracle/readout.py)
+
+
+def test_readout_linear_matches_definition_and_orientation():
+    """linear(x, w) is x . w^T: an elementwise f64 sum by the definition, and
+    a transposed (square) weight gives a different answer."""
+    from oracle.readout import linear
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((3, 6)).astype(np.float32)
+    w = rng.standard_normal((6, 6)).astype(np.float32)
+    want = np.array([[sum(float(x[i, e]) * float(w[j, e]) for e in range(6)) for j in range(6)] for i in range(3)], np.float32)
+    assert np.array_equal(linear(x, w, False), want)
+    assert not np.allclose(linear(x, w.T, False), want)
+    # bf16: the f32 result rounded once
+    assert np.array_equal(linear(x, w, True), oracle.round_bf16(want))
+
+
+def test_d3_readout_composition_and_temperature():
+    """d3_readout = (o_rows . wo^T in the model dtype) . wr^T times the f32
+    1 / temperature: a one-hot o row picks one column of wo, and halving the
+    temperature doubles every logit exactly."""
+    from oracle.readout import d3_readout, inv_temperature
+    rng = np.random.default_rng(2)
+    wo = rng.standard_normal((5, 8)).astype(np.float32)
+    wr = rng.standard_normal((7, 5)).astype(np.float32)
+    o = np.zeros((1, 8), np.float32)
+    o[0, 3] = 1.0
+    z = d3_readout(o, wo, wr, 1.0, False)
+    assert np.allclose(z[0], (wr.astype(np.float64) @ wo[:, 3].astype(np.float64)), rtol=1e-6, atol=1e-6)
+    assert np.array_equal(d3_readout(o, wo, wr, 0.5, False), 2 * z)
+    assert inv_temperature(0.8) == np.float32(1.0 / np.float64(np.float32(0.8)))
+
+
+# ---------------------------------------------------------------------------
+# Packed-pass engine (oracle/engine.py)
+
+
+def _tiny_stack(bf16=False):
+    from cev_hip import configs
+    return configs.Qwen3StackWorkload("tiny", 9, bf16, n_layers=2, hidden=256, hq=4, hkv=2, d=128, inter=512, vocab=512)
+
+
+def test_oracle_engine_packing_is_asking_each_request_alone(orc):
+    """README.md:47 / qwen3.rs:13-17: packing several plans and their
+    questions into passes is exactly asking each one alone.  A request and
+    its calibration twin in one call (two plans, two tails, 3 passes under a
+    small token budget) give the same logits as each request in a call of
+    its own.  The comparison is sensitive: a planted error in the pass mask
+    (a question token missing its own key) moves the logits beyond it."""
+    from oracle.engine import OracleEngine
+    from oracle.qwen3_stack import Qwen3Oracle
+    w = _tiny_stack()
+    W = w.weights()
+    rng = np.random.default_rng(0)
+    a = (rng.integers(0, w.vocab, 700), [rng.integers(0, w.vocab, int(rng.integers(3, 20))) for _ in range(5)])
+    b = (rng.integers(0, w.vocab, 90), [rng.integers(0, w.vocab, int(rng.integers(3, 20))) for _ in range(5)])
+    codes = [3, 17, 99, 200]
+    both = OracleEngine(Qwen3Oracle(w, W), 10_000, codes, pass_tokens=300).run_many([a, b])
+    alone_a = OracleEngine(Qwen3Oracle(w, W), 10_000, codes).run_many([a])[0]
+    alone_b = OracleEngine(Qwen3Oracle(w, W), 10_000, codes).run_many([b])[0]
+    assert np.allclose(both[0]["logits"], alone_a["logits"], rtol=0, atol=2e-5)
+    assert np.allclose(both[1]["logits"], alone_b["logits"], rtol=0, atol=2e-5)
+    with oracle.mutation(oracle.MUT_MASK_NO_DIAG):
+        bad = OracleEngine(Qwen3Oracle(w, W), 10_000, codes, pass_tokens=300).run_many([a, b])
+    assert not np.allclose(bad[0]["logits"], alone_a["logits"], rtol=0, atol=2e-5)
+
+
+def test_oracle_engine_cache_hit_reproduces_the_miss(orc):
+    """A second call on a cached prefix (no prefill, no tail) gives the
+    first call's logits for the same questions (parity_models.rs:60-67
+    holds the reference to 1e-4 here)."""
+    from oracle.engine import OracleEngine
+    from oracle.qwen3_stack import Qwen3Oracle
+    w = _tiny_stack()
+    eng = OracleEngine(Qwen3Oracle(w, w.weights()), 10_000, [1, 2, 3])
+    rng = np.random.default_rng(1)
+    req = (rng.integers(0, w.vocab, 600), [rng.integers(0, w.vocab, 12) for _ in range(3)])
+    first = eng.run_many([req])[0]
+    second = eng.run_many([req])[0]
+    assert not first["prefix_cached"] and second["prefix_cached"]
+    assert np.allclose(first["logits"], second["logits"], rtol=0, atol=1e-5)

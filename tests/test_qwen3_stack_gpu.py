@@ -29,22 +29,38 @@ def _say(msg):
     print(msg, flush=True)
 
 
-def _gpu_config(w, weights, device, second_pass=False):
-    """The config-2 flow on the device.  Returns (probabilities, hidden, stack)."""
-    import torch
-
-    from cev_hip import BlockTable
-    from cev_hip.qwen3 import Qwen3Stack, softmax64
+def _request(w):
     state, qs, codes = w.ids()
-    stack = Qwen3Stack(w, weights, device, capacity=w.state_tokens + w.questions * w.q_len)
-    stack.prefill(state[: w.head_tokens], w.prefill_chunk)
-    plans, items = w.plans_items()
-    table, pos, gather = BlockTable.from_plans(plans, items)
-    tokens = np.concatenate([state[w.head_tokens:], qs.reshape(-1)])
-    hid = stack.forward_packed(tokens, pos, table, gather, keep_tokens=w.state_tokens - w.head_tokens)
-    logits = stack.code_logits(hid, codes)
-    torch.cuda.synchronize()
-    return softmax64(to_np(logits)), to_np(hid), stack
+    return (state, list(qs)), codes
+
+
+def _gpu_engine(w, weights, device, budget=None, pass_tokens=None, capacity=None):
+    from cev_hip.engine import DeviceEngine
+    from cev_hip.qwen3 import Qwen3Stack
+    stack = Qwen3Stack(w, weights, device, capacity=capacity or (w.state_tokens + w.questions * w.q_len))
+    _, codes = _request(w)
+    return DeviceEngine(stack, budget=budget or w.state_tokens, code_ids=codes, pass_tokens=pass_tokens or w.pass_tokens,
+                        prefill_chunk=w.prefill_chunk)
+
+
+def _gpu_config(w, weights, device):
+    """The config-2 flow on the device through the engine (prefill of the
+    head into the prefix store's slots, one packed pass of the tail and the
+    questions).  Returns (probabilities, hidden, engine)."""
+    from cev_hip.qwen3 import softmax64
+    eng = _gpu_engine(w, weights, device)
+    req, _ = _request(w)
+    r = eng.run_many([req])[0]
+    assert eng.passes == 1 and not r["prefix_cached"]
+    return softmax64(r["logits"]), r["hidden"], eng
+
+
+def _oracle_engine(w, weights, budget=None, pass_tokens=None):
+    from oracle.engine import OracleEngine
+    from oracle.qwen3_stack import Qwen3Oracle
+    _, codes = _request(w)
+    return OracleEngine(Qwen3Oracle(w, weights), budget or w.state_tokens, codes, pass_tokens=pass_tokens or w.pass_tokens,
+                        prefill_chunk=w.prefill_chunk)
 
 
 @pytest.mark.parametrize("bf16", [False, True])
@@ -91,60 +107,89 @@ def test_swiglu_matches_oracle(gpu, bf16):
 @pytest.mark.parametrize("bf16", [False, True])
 def test_stack_two_layers_vs_oracle(gpu, orc, bf16):
     """Config 2's widths and token layout at 2 layers and a 4096-token vocab."""
-    from oracle.qwen3_stack import Qwen3Oracle, softmax64
+    from oracle.qwen3_stack import softmax64
     w = configs.c2(bf16, n_layers=2, vocab=4096)
     _say(f"test stack: bf16={bf16} layers={w.n_layers} hidden={w.hidden} state={w.state_tokens} pass={w.pass_tokens}")
     weights = w.weights()
-    p, hid, stack = _gpu_config(w, weights, gpu)
-    o = Qwen3Oracle(w, weights)
-    state, qs, codes = w.ids()
-    o.prefill(state[: w.head_tokens], w.prefill_chunk)
-    plans, items = w.plans_items()
-    rh = o.forward_packed(plans, items, np.concatenate([state[w.head_tokens:], qs.reshape(-1)]))
-    rp = softmax64(o.code_logits(rh, codes))
+    p, hid, eng = _gpu_config(w, weights, gpu)
+    oe = _oracle_engine(w, weights)
+    req, _ = _request(w)
+    r = oe.run_many([req])[0]
+    rp, rh = softmax64(r["logits"]), r["hidden"]
     dp = float(np.abs(p - rp).max())
     dh = float(np.abs(hid - rh).max())
     scale = float(np.abs(rh).max())
-    # the cached K/V after the pass: head (prefill) + tail (kept from the pass), layer 1
-    kc = to_np(stack.layers[1]["k"][:, : w.state_tokens])
-    vc = to_np(stack.layers[1]["v"][:, : w.state_tokens])
-    dk = float(np.abs(kc - o.past[1][0]).max())
-    dv = float(np.abs(vc - o.past[1][1]).max())
+    # the cached K/V of the prefix after the pass: head (prefill) + tail
+    # (kept from the pass), at the slots the store gave it, layer 1
+    (begin, n), = eng.store.entries()
+    assert n == w.state_tokens
+    L1 = eng.stack.layers[1]
+    kc, vc = to_np(L1["k"][:, begin: begin + n]), to_np(L1["v"][:, begin: begin + n])
+    (_, okv), = oe.cache.entries
+    dk = float(np.abs(kc - okv[1][0]).max())
+    dv = float(np.abs(vc - okv[1][1]).max())
     _say(f"  |dp| {dp:.3g}  max|dhidden| {dh:.3g} (|hidden| <= {scale:.3g})  cache |dk| {dk:.3g} |dv| {dv:.3g}")
-    assert stack.cached == w.state_tokens
     if bf16:
-        assert dh <= 2e-2 * scale and dk <= 2e-2 * float(np.abs(o.past[1][0]).max())
+        assert dh <= 2e-2 * scale and dk <= 2e-2 * float(np.abs(okv[1][0]).max())
     else:
         assert dp < P_TOL
         assert dh <= HID_F32_TOL and dk <= HID_F32_TOL and dv <= HID_F32_TOL
 
 
 def test_stack_second_pass_reads_the_cached_prefix(gpu, orc):
-    """A later request on the same state: the whole state is cached (no tail),
-    the questions attend to the device cache the first pass left behind."""
-    from cev_hip import BlockTable
-    from cev_hip.qwen3 import softmax64
-    from oracle.qwen3_stack import Qwen3Oracle
-    from oracle.qwen3_stack import softmax64 as osoftmax
+    """A later request on the same state: the whole state is a store hit (no
+    prefill, no tail) and new questions attend to the slots the first call
+    left behind."""
+    from oracle.qwen3_stack import softmax64
     w = configs.c2(False, n_layers=2, vocab=4096, questions=8)
     weights = w.weights()
-    _, _, stack = _gpu_config(w, weights, gpu)
-    o = Qwen3Oracle(w, weights)
-    state, qs, codes = w.ids()
-    o.prefill(state[: w.head_tokens], w.prefill_chunk)
-    plans, items = w.plans_items()
-    o.forward_packed(plans, items, np.concatenate([state[w.head_tokens:], qs.reshape(-1)]))
-    # second pass: new questions (reversed token order), cached prefix only
-    q2 = qs[:, ::-1].copy()
-    plans2 = [(w.state_tokens, w.state_tokens, w.state_tokens)]
-    table, pos, gather = BlockTable.from_plans(plans2, items)
-    hid = stack.forward_packed(q2.reshape(-1), pos, table, gather)
-    p = softmax64(to_np(stack.code_logits(hid, codes)))
-    rh = o.forward_packed(plans2, items, q2.reshape(-1))
-    rp = osoftmax(o.code_logits(rh, codes))
-    dp = float(np.abs(p - rp).max())
-    _say(f"test second pass: |dp| {dp:.3g}, max|dhidden| {float(np.abs(to_np(hid) - rh).max()):.3g}")
+    _, _, eng = _gpu_config(w, weights, gpu)
+    oe = _oracle_engine(w, weights)
+    (state, qs), _ = _request(w)
+    oe.run_many([(state, qs)])
+    q2 = [q[::-1].copy() for q in qs]
+    r = eng.run_many([(state, q2)])[0]
+    ro = oe.run_many([(state, q2)])[0]
+    assert r["prefix_cached"] and ro["prefix_cached"]
+    dp = float(np.abs(softmax64(r["logits"]) - softmax64(ro["logits"])).max())
+    _say(f"test second pass: |dp| {dp:.3g}, max|dhidden| {float(np.abs(r['hidden'] - ro['hidden']).max()):.3g}")
     assert dp < P_TOL
+
+
+def test_engine_request_and_twin_then_eviction(gpu, orc):
+    """Row f2: a request and its content-free calibration twin (two plans,
+    two tails) in one call, split into passes by the token budget,
+    through the device prefix store (the first call needs more than one
+    pass under the 1000-token budget); then a second call where the request's
+    prefix is a hit and a new twin's put evicts the first twin (LRU by
+    tokens).  f32 probabilities against the oracle engine at |dp| < 5e-5,
+    and the store's entries against the oracle's PrefixCache."""
+    from oracle.qwen3_stack import softmax64
+    w = configs.c2(False, n_layers=2, vocab=4096, questions=6, q_len=20)
+    weights = w.weights()
+    rng = np.random.default_rng(12)
+    qs = [rng.integers(0, w.vocab, int(rng.integers(8, 30))) for _ in range(6)]
+    req = (rng.integers(0, w.vocab, 1100), qs)
+    twin = (rng.integers(0, w.vocab, 300), qs)
+    twin2 = (rng.integers(0, w.vocab, 420), qs)
+    budget = 1100 + 300 + 420 - 1
+    eng = _gpu_engine(w, weights, gpu, budget=budget, pass_tokens=1000, capacity=4096)
+    oe = _oracle_engine(w, weights, budget=budget, pass_tokens=1000)
+    worst = 0.0
+    passes = []
+    for call, reqs in enumerate(([req, twin], [req, twin2])):
+        got = eng.run_many(reqs)
+        passes.append(eng.passes)
+        want = oe.run_many(reqs)
+        for g, r in zip(got, want):
+            assert g["prefix_cached"] == r["prefix_cached"]
+            worst = max(worst, float(np.abs(softmax64(g["logits"]) - softmax64(r["logits"])).max()))
+        lens = [n for _, n in eng.store.entries()]
+        assert lens == [len(k) for k, _ in oe.cache.entries], (call, lens)
+        _say(f"call {call}: cached={[g['prefix_cached'] for g in got]} entries={lens} passes={eng.passes} |dp| {worst:.3g}")
+    assert eng.passes == oe.passes and passes[0] >= 2
+    assert [len(k) for k, _ in oe.cache.entries] == [1100, 420]  # the first twin was evicted
+    assert worst < P_TOL
 
 
 @pytest.mark.skipif(not os.path.exists(GOLDEN), reason="tests/golden/c2_f32.npz not generated")
