@@ -261,14 +261,21 @@ int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, const void* z,
 /* RMSNorm of `rows` rows of `hidden` elements, candle_nn RmsNorm in the
  * model dtype (input_layernorm / post_attention_layernorm / final norm,
  * crates/cev-model/src/qwen3.rs:254-255, :400): y = dtype(dtype(x / m) * w),
- * m = dtype(sqrt(sum x^2 / hidden + eps)), the sum in element order.
+ * m = dtype(sqrt(sum x^2 / hidden + eps)).
  * With h != NULL the residual add before the norm is fused in
  * (qwen3.rs:261 in mlp_block, :358 and :397): x_out = dtype(x + h) is written
  * (x_out may alias x) and normalised.  weight_plus_one selects 1 + w.
- * Strides are in elements; rows and buffers 16-byte aligned. */
+ * Strides are in elements; rows and buffers 16-byte aligned.
+ * cev_rms_norm sums the squares in tree order (one wave per row; rows up to
+ * 16 x 64 16-byte chunks, wider rows take the sequential sum);
+ * cev_rms_norm_seq sums them in element order like candle's CPU kernel, so
+ * its results are the sequential sum's bit for bit (validation). */
 int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h, int64_t h_stride,
                      void* x_out, int64_t x_out_stride, const void* w, float eps, int32_t weight_plus_one, void* y, int64_t y_stride,
                      cev_stream stream);
+int32_t cev_rms_norm_seq(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h, int64_t h_stride,
+                         void* x_out, int64_t x_out_stride, const void* w, float eps, int32_t weight_plus_one, void* y, int64_t y_stride,
+                         cev_stream stream);
 
 /* The SwiGLU of Mlp::forward (qwen3.rs:230-233): out = dtype(silu(gate) * up),
  * silu(v) = v / (1 + exp(-v)) with each op in the model dtype.  gate and up

@@ -369,11 +369,13 @@ def qknorm_rope_kv(q_in, k_in, v_in, w_q, w_k, pos, rot: Rotary, eps: float, q_o
     return q_out, k_out, v_out
 
 
-def rms_norm(x, w, eps: float, h=None, x_out=None, y=None, plus_one: bool = False, stream=None):
+def rms_norm(x, w, eps: float, h=None, x_out=None, y=None, plus_one: bool = False, stream=None, sequential: bool = False):
     """candle_nn RmsNorm over the last dim of a (rows, hidden) view in the
     model dtype (qwen3.rs:254-255, :400); with h, the residual add before it
     (qwen3.rs:261, :358, :397): x_out = x + h is written (x_out may be x)
-    and normalised.  Returns y."""
+    and normalised.  sequential=True sums the squares in element order
+    (cev_rms_norm_seq, candle's CPU order bit for bit) instead of tree order.
+    Returns y."""
     torch = _torch()
     rows, hidden = x.shape
     if y is None:
@@ -383,7 +385,8 @@ def rms_norm(x, w, eps: float, h=None, x_out=None, y=None, plus_one: bool = Fals
     for t_ in (x, y, w) + ((h, x_out) if h is not None else ()):
         if t_.stride(-1) != 1 or t_.dtype != x.dtype:
             raise CevError(-2, "rms_norm: tensors must share the dtype and have a contiguous last dim")
-    check(lib().cev_rms_norm(_dtype_code(x), rows, hidden, _ptr(x), x.stride(0), _ptr(h), h.stride(0) if h is not None else 0,
+    fn = lib().cev_rms_norm_seq if sequential else lib().cev_rms_norm
+    check(fn(_dtype_code(x), rows, hidden, _ptr(x), x.stride(0), _ptr(h), h.stride(0) if h is not None else 0,
                              _ptr(x_out), x_out.stride(0) if x_out is not None else 0, _ptr(w), float(eps), 1 if plus_one else 0,
                              _ptr(y), y.stride(0), _stream_ptr(stream)))
     return y

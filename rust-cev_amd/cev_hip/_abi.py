@@ -106,6 +106,7 @@ SIGNATURES = {
     "cev_gdn_workspace_size": (i32, [C.POINTER(GdnDesc), C.POINTER(C.c_size_t)]),
     "cev_gdn_forward": (i32, [C.POINTER(GdnDesc), P, P, P, P, P, P, P, P, P, P, P, P, P, P, C.c_size_t, P]),
     "cev_rms_norm": (i32, [i32, i64, i32, P, i64, P, i64, P, i64, P, C.c_float, i32, P, i64, P]),
+    "cev_rms_norm_seq": (i32, [i32, i64, i32, P, i64, P, i64, P, i64, P, C.c_float, i32, P, i64, P]),
     "cev_swiglu": (i32, [i32, i64, i32, P, P, i64, P, i64, P]),
     "cev_debias_scores": (i32, [i32, i32, P, P, P, P, P, P, i32, P, P]),
     "cev_blas_create": (i32, [C.POINTER(P)]),

@@ -11,7 +11,15 @@
 //                 op in the model dtype (Mlp::forward, qwen3.rs:230-233).
 // The projections around them are plain GEMMs (the library's).
 //
-// Norm work split: a workgroup takes up to kNormRows rows.  All 1024 threads
+// Two norm kernels.  rms_norm_wave_kernel (cev_rms_norm): one wave per row,
+// each lane keeping its 16-byte chunks in registers; the sum of squares is
+// each lane's partial sum in chunk order, then an xor-butterfly over the
+// wave (tree order: every lane ends with the same bits).  It differs from
+// the reference's sequential f32 sum only in the last bits of the sum.
+// rms_norm_kernel (cev_rms_norm_seq) keeps the reference's element order
+// bit for bit.
+//
+// Sequential-sum work split: a workgroup takes up to kNormRows rows.  All 1024 threads
 // load them with coalesced 16-byte accesses (x + h for the fused residual,
 // written back as they go), keep their chunks in registers and put the
 // squares, as f32, in LDS; lanes 0..rows-1 of wave 0 then each add one row's
@@ -183,6 +191,88 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a, int 
   }
 }
 
+constexpr int kWaveNormRows = 4;  // rows (waves) per workgroup of the wave kernel
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// One wave per row, lane l holding chunks l, l + 64, ... (NCH at most).
+template <typename T, int NCH>
+__global__ __launch_bounds__(kWaveNormRows * 64) void rms_norm_wave_kernel(NormArgs a) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int VEC = 16 / (int)sizeof(T);
+  auto rnd = [](float v) { return BF ? bf16_round(v) : v; };
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * kWaveNormRows + (threadIdx.x >> 6);
+  if (r >= a.rows) return;
+  const int nc = a.hidden / VEC;
+  u32x4 cx[NCH], ch[NCH];
+#pragma unroll
+  for (int b = 0; b < NCH; ++b) {
+    const int k = lane + 64 * b;
+    if (k < nc) {
+      cx[b] = *(const u32x4*)((const T*)a.x + r * a.x_st + k * VEC);
+      if (a.h) ch[b] = *(const u32x4*)((const T*)a.h + r * a.h_st + k * VEC);
+    }
+  }
+  float s = 0.0f;
+  int me = 0;
+#pragma unroll
+  for (int b = 0; b < NCH; ++b) {
+    const int k = lane + 64 * b;
+    if (k < nc) {
+      float xs[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) xs[j] = a.h ? rnd(elem<T>(cx[b], j) + elem<T>(ch[b], j)) : elem<T>(cx[b], j);
+      if (a.h) {
+        cx[b] = pack<T>(xs);
+        *(u32x4*)((T*)a.x_out + r * a.xo_st + k * VEC) = cx[b];
+      }
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        s = __builtin_fmaf(xs[j], xs[j], s);
+        me = min(me, __builtin_amdgcn_frexp_expf(xs[j]));
+      }
+    }
+  }
+  s = wave_sum_f32(s);
+  me = wave_min_i32(me);
+  const float m = rnd(sqrtf(s / (float)a.hidden + a.eps));
+  const float y = 1.0f / m;
+  const bool fast = me >= -95 && s <= 0x1p120f && m >= 0x1p-20f && m <= 0x1p20f;
+#pragma unroll
+  for (int b = 0; b < NCH; ++b) {
+    const int k = lane + 64 * b;
+    if (k < nc) {
+      const u32x4 cw = *(const u32x4*)((const T*)a.w + k * VEC);
+      float ys[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float x = elem<T>(cx[b], j);
+        float q;
+        if (fast) {
+          const float q0 = x * y;
+          q = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, m, x), y, q0), q0);
+        } else {
+          q = x / m;
+        }
+        float w = elem<T>(cw, j);
+        if (a.plus_one) w = rnd(w + 1.0f);
+        ys[j] = rnd(rnd(q) * w);
+      }
+      *(u32x4*)((T*)a.y + r * a.y_st + k * VEC) = pack<T>(ys);
+    }
+  }
+}
+
 struct SwigluArgs {
   const void* g;
   const void* u;
@@ -296,9 +386,10 @@ __global__ __launch_bounds__(64) void debias_kernel(DebiasArgs a) {
 
 }  // namespace
 
-extern "C" int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h,
-                                int64_t h_stride, void* x_out, int64_t x_out_stride, const void* w, float eps, int32_t weight_plus_one,
-                                void* y, int64_t y_stride, cev_stream stream) {
+namespace {
+
+int32_t check_norm(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h, int64_t h_stride,
+                   void* x_out, int64_t x_out_stride, const void* w, float eps, void* y, int64_t y_stride) {
   if (dtype != CEV_F32 && dtype != CEV_BF16) return cev_fail(CEV_ERR_UNSUPPORTED, "cev_rms_norm: dtype %d", dtype);
   const int vec = dtype == CEV_BF16 ? 8 : 4;
   CEV_CHECK_ARG(rows >= 0 && hidden > 0 && hidden % vec == 0, "cev_rms_norm: hidden %d must be a positive multiple of %d", hidden, vec);
@@ -310,6 +401,13 @@ extern "C" int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, con
   CEV_CHECK_ARG(x_stride >= hidden && y_stride >= hidden && x_stride % vec == 0 && y_stride % vec == 0 &&
                     (!h || (h_stride >= hidden && x_out_stride >= hidden && h_stride % vec == 0 && x_out_stride % vec == 0)),
                 "cev_rms_norm: row strides must cover a row and keep rows 16-byte aligned");
+  return CEV_OK;
+}
+
+int32_t rms_norm_seq(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h, int64_t h_stride,
+                     void* x_out, int64_t x_out_stride, const void* w, float eps, int32_t weight_plus_one, void* y, int64_t y_stride,
+                     cev_stream stream) {
+  const int vec = dtype == CEV_BF16 ? 8 : 4;
   NormArgs a{x, h, x_out, w, y, rows, x_stride, h_stride, x_out_stride, y_stride, hidden, weight_plus_one, eps};
   const int pitch = norm_pitch(hidden);
   const int rows_per_wg = std::min({kNormRows, kNormLdsBytes / pitch, kNormThreads * kNormChunks / (hidden / vec)});
@@ -325,6 +423,46 @@ extern "C" int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, con
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "cev_rms_norm launch: %s", hipGetErrorString(e));
   return CEV_OK;
+}
+
+template <typename T>
+int32_t launch_wave_norm(const NormArgs& a, int nch, hipStream_t s) {
+  const int64_t grid = (a.rows + kWaveNormRows - 1) / kWaveNormRows;
+  if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "cev_rms_norm: too many rows");
+  const dim3 g((unsigned)grid), b(kWaveNormRows * 64);
+  if (nch <= 4)
+    hipLaunchKernelGGL((rms_norm_wave_kernel<T, 4>), g, b, 0, s, a);
+  else if (nch <= 8)
+    hipLaunchKernelGGL((rms_norm_wave_kernel<T, 8>), g, b, 0, s, a);
+  else
+    hipLaunchKernelGGL((rms_norm_wave_kernel<T, 16>), g, b, 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "cev_rms_norm launch: %s", hipGetErrorString(e));
+  return CEV_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t cev_rms_norm(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h,
+                                int64_t h_stride, void* x_out, int64_t x_out_stride, const void* w, float eps, int32_t weight_plus_one,
+                                void* y, int64_t y_stride, cev_stream stream) {
+  int32_t rc = check_norm(dtype, rows, hidden, x, x_stride, h, h_stride, x_out, x_out_stride, w, eps, y, y_stride);
+  if (rc || rows == 0) return rc;
+  const int vec = dtype == CEV_BF16 ? 8 : 4;
+  const int nch = (hidden / vec + 63) / 64;  // 16-byte chunks per lane
+  if (nch > 16)  // rows wider than 16 chunks per lane: the sequential-sum kernel
+    return rms_norm_seq(dtype, rows, hidden, x, x_stride, h, h_stride, x_out, x_out_stride, w, eps, weight_plus_one, y, y_stride, stream);
+  NormArgs a{x, h, x_out, w, y, rows, x_stride, h_stride, x_out_stride, y_stride, hidden, weight_plus_one, eps};
+  if (dtype == CEV_BF16) return launch_wave_norm<uint16_t>(a, nch, (hipStream_t)stream);
+  return launch_wave_norm<float>(a, nch, (hipStream_t)stream);
+}
+
+extern "C" int32_t cev_rms_norm_seq(int32_t dtype, int64_t rows, int32_t hidden, const void* x, int64_t x_stride, const void* h,
+                                    int64_t h_stride, void* x_out, int64_t x_out_stride, const void* w, float eps, int32_t weight_plus_one,
+                                    void* y, int64_t y_stride, cev_stream stream) {
+  int32_t rc = check_norm(dtype, rows, hidden, x, x_stride, h, h_stride, x_out, x_out_stride, w, eps, y, y_stride);
+  if (rc || rows == 0) return rc;
+  return rms_norm_seq(dtype, rows, hidden, x, x_stride, h, h_stride, x_out, x_out_stride, w, eps, weight_plus_one, y, y_stride, stream);
 }
 
 extern "C" int32_t cev_swiglu(int32_t dtype, int64_t rows, int32_t inter, const void* gate, const void* up, int64_t in_stride, void* out,

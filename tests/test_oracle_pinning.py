@@ -8,6 +8,7 @@ test plants a plausible mistake in the oracle (cev_oracle.c MUT_*) and shows
 that the same check then fails.
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -645,3 +646,33 @@ def test_oracle_engine_cache_hit_reproduces_the_miss(orc):
     second = eng.run_many([req])[0]
     assert not first["prefix_cached"] and second["prefix_cached"]
     assert np.allclose(first["logits"], second["logits"], rtol=0, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# Config 2 against HF transformers (tests/golden/make_c2_hf.py)
+
+HF_GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "c2_hf_f32.npz")
+
+
+@pytest.mark.skipif(not os.path.exists(HF_GOLDEN), reason="tests/golden/c2_hf_f32.npz not generated")
+def test_c2_oracle_matches_hf_transformers(orc):
+    """The Qwen3 stack oracle's composition (layer order, residual
+    placement, QK-norm + RoPE, the engine's chunked head prefill and packed
+    pass, final norm at the gather rows, tied code head) against
+    Qwen3ForCausalLM asked each question alone over [state || question], on
+    config 2's seeded weights at 2 layers: the reference's own pin of its
+    f32 path (README.md:48, |dp| < 5e-5)."""
+    from cev_hip import configs
+    from oracle.engine import OracleEngine
+    from oracle.qwen3_stack import Qwen3Oracle, softmax64
+    g = np.load(HF_GOLDEN)
+    w = configs.c2(False, n_layers=int(g["layers"]), vocab=int(g["vocab"]), questions=int(g["questions"]))
+    state, qs, codes = w.ids()
+    eng = OracleEngine(Qwen3Oracle(w, w.weights()), w.state_tokens, codes, pass_tokens=w.pass_tokens, prefill_chunk=w.prefill_chunk)
+    r = eng.run_many([(state, list(qs))])[0]
+    dp = float(np.abs(softmax64(r["logits"]) - g["p"]).max())
+    dh = float(np.abs(r["hidden"] - g["hidden"]).max())
+    print(f"oracle vs HF: |dp| {dp:.3g}, max|dhidden| {dh:.3g} (|hidden| <= {float(np.abs(g['hidden']).max()):.3g})")
+    assert eng.passes == 1
+    assert dp < 5e-5
+    assert dh < 1e-3

@@ -23,6 +23,9 @@ pytestmark = pytest.mark.gpu
 P_TOL = 5e-5
 HID_F32_TOL = 1e-4
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "c2_f32.npz")
+GOLDEN_BF16 = os.path.join(os.path.dirname(__file__), "golden", "c2_bf16.npz")
+HF_GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "c2_hf_f32.npz")
+BF16_P_TOL = 3e-2  # the reference's |dp| bar for non-f32 runs (parity_models.rs:42)
 
 
 def _say(msg):
@@ -64,11 +67,15 @@ def _oracle_engine(w, weights, budget=None, pass_tokens=None):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("rows,hidden,residual", [(3584, 2048, False), (37, 2048, True), (5, 4096, True), (1, 64, False)])
-def test_layer_norm_bit_exact(gpu, orc, bf16, rows, hidden, residual):
-    """cev_rms_norm (with and without the fused residual add, row counts that
-    leave a partial workgroup) against the oracle's rms_norm bit for bit;
-    x_out aliases x as in the stack."""
+@pytest.mark.parametrize("rows,hidden,residual", [(3584, 2048, False), (37, 2048, True), (5, 4096, True), (1, 64, False),
+                                                  (300, 5120, True), (7, 12288, False)])
+def test_layer_norm_vs_oracle(gpu, orc, bf16, rows, hidden, residual):
+    """cev_rms_norm_seq (the reference's element-order sum) against the
+    oracle's rms_norm bit for bit, and cev_rms_norm (tree-order sum) within
+    a few roundings of it: the two sums differ only in their last f32 bits,
+    so m moves by at most one step of the model dtype and y by a few (row counts
+    that leave a partial workgroup; widths up to and past the wave kernel's
+    16 chunks per lane; x_out aliases x as in the stack)."""
     import cev_hip
     from helpers import to_dev
     rng = np.random.default_rng(rows + hidden)
@@ -77,13 +84,20 @@ def test_layer_norm_bit_exact(gpu, orc, bf16, rows, hidden, residual):
     w = (1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
     if bf16:
         x, h, w = orc.round_bf16(x), orc.round_bf16(h), orc.round_bf16(w)
-    dx, dh, dw = to_dev(x, bf16, gpu), to_dev(h, bf16, gpu), to_dev(w, bf16, gpu)
-    y = cev_hip.rms_norm(dx, dw, 1e-6, h=dh if residual else None, x_out=dx if residual else None)
     xs = (orc.round_bf16(x + h) if bf16 else (x + h)) if residual else x
     want = orc.rms_norm(xs, w, 1e-6, bf16)
-    assert np.array_equal(to_np(y), want)
-    if residual:
-        assert np.array_equal(to_np(dx), xs)
+    step = 2.0 ** -6 if bf16 else 2.0 ** -16
+    for sequential in (True, False):
+        dx, dh, dw = to_dev(x, bf16, gpu), to_dev(h, bf16, gpu), to_dev(w, bf16, gpu)
+        y = cev_hip.rms_norm(dx, dw, 1e-6, h=dh if residual else None, x_out=dx if residual else None, sequential=sequential)
+        got = to_np(y)
+        if residual:
+            assert np.array_equal(to_np(dx), xs)
+        if sequential:
+            assert np.array_equal(got, want)
+        else:
+            err = np.abs(got - want)
+            assert np.all(err <= step * np.abs(want) + 1e-30), float((err / np.maximum(np.abs(want), 1e-30)).max())
 
 
 @pytest.mark.parametrize("bf16", [False, True])
@@ -190,6 +204,44 @@ def test_engine_request_and_twin_then_eviction(gpu, orc):
     assert eng.passes == oe.passes and passes[0] >= 2
     assert [len(k) for k, _ in oe.cache.entries] == [1100, 420]  # the first twin was evicted
     assert worst < P_TOL
+
+
+@pytest.mark.skipif(not os.path.exists(HF_GOLDEN), reason="tests/golden/c2_hf_f32.npz not generated")
+def test_stack_two_layers_vs_hf_transformers(gpu):
+    """The device engine against HF transformers' Qwen3ForCausalLM asked
+    each question alone over [state || question] (tests/golden/make_c2_hf.py),
+    config 2's widths at 2 layers, f32: the reference's own bar
+    (README.md:48)."""
+    from cev_hip.qwen3 import softmax64
+    g = np.load(HF_GOLDEN)
+    w = configs.c2(False, n_layers=int(g["layers"]), vocab=int(g["vocab"]), questions=int(g["questions"]))
+    p, hid, _ = _gpu_config(w, w.weights(), gpu)
+    dp = float(np.abs(p - g["p"]).max())
+    dh = float(np.abs(hid - g["hidden"]).max())
+    _say(f"stack vs HF transformers: |dp| {dp:.3g}  max|dhidden| {dh:.3g}")
+    assert dp < P_TOL and dh < 1e-3
+
+
+@pytest.mark.skipif(not os.path.exists(GOLDEN_BF16), reason="tests/golden/c2_bf16.npz not generated")
+def test_config2_full_bf16_vs_golden(gpu):
+    """All 28 layers and the full vocab in bf16 (the config's own dtype)
+    against the oracle's bf16 fixture: |dp| <= 3e-2, the bar the reference
+    holds its own non-f32 runs to (parity_models.rs:42).  The hidden state
+    is reported and held to 10 % of its norm (relative RMS): the device
+    keeps attention scores in f32 where candle rounds them to bf16, and
+    rounds f32 GEMM sums taken in another order, so every layer moves some
+    elements by a bf16 step and 28 residual layers accumulate it (about
+    1.4 % at 2 layers, 4.6 % at 28)."""
+    w = configs.c2(True)
+    g = np.load(GOLDEN_BF16)
+    _say(f"test config 2 full bf16: layers={w.n_layers} vocab={w.vocab}")
+    p, hid, _ = _gpu_config(w, w.weights(), gpu)
+    dp = float(np.abs(p - g["p"]).max())
+    dh = float(np.abs(hid - g["hidden"]).max())
+    rel = float(np.linalg.norm(hid - g["hidden"]) / np.linalg.norm(g["hidden"]))
+    scale = float(np.abs(g["hidden"]).max())
+    _say(f"  |dp| {dp:.3g}  hidden relative RMS {rel:.3g}, max|dhidden| {dh:.3g} (|hidden| <= {scale:.3g})")
+    assert dp <= BF16_P_TOL and rel <= 0.1
 
 
 @pytest.mark.skipif(not os.path.exists(GOLDEN), reason="tests/golden/c2_f32.npz not generated")
