@@ -489,3 +489,34 @@ def test_qknorm_rope_bit_exact_on_extreme_values(gpu, orc, bf16, d, rot, plus_on
             idx = np.argwhere(bad)[:5]
             _say(f"{name} mismatches at {idx.tolist()}: got {got[tuple(idx.T)]}, want {want[tuple(idx.T)]}")
         assert _same_bits(got, want), name
+
+
+def test_split_records_are_never_stale(gpu):
+    """Split parts write partial records that the merge pass reads.  A
+    second call on the same plan and workspace with new K/V in the same
+    buffers must merge the new records, not the first call's: each call is
+    compared with an unsplit run of its own inputs (the merge may differ
+    from it only in the last bits).  hkv = 4 puts the parts of one tile on
+    two XCDs."""
+    import torch
+    for prefix, t, hq, hkv, d, dtype, gated in ((32768, 16, 32, 8, 128, torch.bfloat16, False),
+                                                (4096, 128, 16, 4, 256, torch.bfloat16, True),
+                                                (256, 32, 16, 8, 128, torch.float32, False)):
+        g = torch.Generator(device="cpu").manual_seed(t)
+        rnd = lambda *s: torch.randn(*s, generator=g).to(dtype).to(gpu)  # noqa: E731
+        q, kn, vn = rnd(t, hq, d), rnd(t, hkv, d), rnd(t, hkv, d)
+        kc, vc = rnd(hkv, prefix, d), rnd(hkv, prefix, d)
+        gate = rnd(t, hq, d) if gated else None
+        tab = cev_hip.BlockTable.from_rows(1, t, prefix, causal=True)
+        op = cev_hip.PackedAttention(q, kn, tab, k_cache=kc, s_cache=prefix, v_new=vn, v_cache=vc, has_gate=gated, gate=gate)
+        ref = cev_hip.PackedAttention(q, kn, tab, k_cache=kc, s_cache=prefix, v_new=vn, v_cache=vc, has_gate=gated, gate=gate,
+                                      max_splits=1)
+        assert op.plan.n_splits > 1 and ref.plan.n_splits == 1
+        for call in range(3):
+            got = op(q, kn, vn, kc, vc, gate).float()
+            want = ref(q, kn, vn, kc, vc, gate).float()
+            err = float((got - want).abs().max())
+            _say(f"stale check hkv={hkv} d={d} {dtype} parts={op.plan.n_splits} call {call}: max|split - unsplit| {err:.3g}")
+            assert err <= (1e-5 if dtype == torch.float32 else 1e-2)
+            kc.copy_(rnd(hkv, prefix, d))  # new keys and values in place
+            vc.copy_(rnd(hkv, prefix, d) * (call + 2))
