@@ -241,24 +241,90 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
-struct __attribute__((aligned(16))) PrepLds {
+constexpr int kSB = 136;  // LDS row stride (bf16 elements) of the raw 128-wide q / k rows
+
+struct __attribute__((aligned(16))) PrepLdsBase {
   float Qs[kC * kSX];  // q normalised * dk^-0.5; later k_cumdecay staging
   float Ks[kC * kSX];  // k normalised
   float Us[kC * kSC];  // ut, strict lower (tiles at and below the diagonal)
   float Iv[kC * kSC];  // (I + ut)^-1 (tiles at and below the diagonal)
-  float Tm[kC * kSC];  // products of the block inversion
-  float In[kC * kSC];  // intra tiles on their way to record order
+  // Products of the block inversion.  Before the inversion (the tile phase)
+  // the same space holds the intra tiles on their way to record order.
+  float Tm[kC * kSC];
   float betas[kC], cums[kC], ecum[kC], ekd[kC];
 };
+// bf16 models also keep the raw q / k rows (the conv output, exact in bf16)
+// for the tile products, with each row's l2norm factor.
+template <bool BF>
+struct PrepLds : PrepLdsBase {};
+template <>
+struct __attribute__((aligned(16))) PrepLds<true> : PrepLdsBase {
+  __bf16 Qb[kC * kSB];
+  __bf16 Kb[kC * kSB];
+  float qf[kC];  // dk^-0.5 / |q_i|
+  float kf[kC];  // 1 / |k_i|
+};
 
-// One 16x16 tile (ti, tj), tj <= ti, of G = (k beta) k^T (DG) and / or
-// QK = q k^T (DQ).  The k-sum runs in the order 16j + 4fq + e, so each lane
-// reads its A and B operands as 16-byte vectors.  Epilogue:
+// Epilogue of one 16x16 tile (ti, tj), tj <= ti, in the MFMA accumulator
+// layout (lane: column 16 tj + fm, rows 16 ti + 4 fq + e):
 //   ut[i][j] = G[i][j] pair[i][j] for j < i,   pair = e^(cum_i - cum_j),
 //   intra[i][j] = QK[i][j] pair[i][j] for j <= i  (qwen35.rs:318-330),
-// ut into Us; intra through the wave's own In tile into its record order.
+// ut into Us; intra through the wave's own tile of Tm into its record order.
+template <bool DG, bool DQ, typename LT>
+__device__ __forceinline__ void prep_tile_store(LT& L, float* rec, int ti, int tj, int lane, const f32x4v& gacc, const f32x4v& qacc) {
+  const int fm = lane & 15, fq = lane >> 4;
+  const int j = 16 * tj + fm;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = 16 * ti + 4 * fq + e;
+    const float pair = j <= i ? expf(L.cums[i] - L.cums[j]) : 0.0f;
+    if (DG) L.Us[i * kSC + j] = j < i ? gacc[e] * pair : 0.0f;
+    if (DQ) L.Tm[i * kSC + j] = qacc[e] * pair;
+  }
+  if (DQ) {
+    wave_lds_sync();
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = L.Tm[(16 * ti + fm) * kSC + 16 * tj + 4 * e + fq];
+    *(f32x4*)(rec + kRecIn + 4 * ((ti * 4 + tj) * 64 + lane)) = v;
+  }
+}
+
+// The tile products for bf16 models: G = (k beta) k^T and QK = q k^T on
+// v_mfma_f32_16x16x32_bf16 over the raw bf16 rows (every product of two
+// bf16 values is exact in f32 and the sums are f32, as with the normalised
+// f32 operands), then the l2norm factors and beta:
+//   G[i][j] = (k_i . k_j) (beta_i / |k_i|) / |k_j|,  QK[i][j] = (q_i . k_j) (dk^-0.5 / |q_i|) / |k_j|.
+// Lane (fm, fq) reads row 16 t + fm, columns 32 s + 8 fq .. + 7 (16 bytes)
+// of A and B, so both operands pair up over the same k.
 template <bool DG, bool DQ>
-__device__ __forceinline__ void prep_tile(PrepLds& L, float* rec, int ti, int tj, int lane) {
+__device__ __forceinline__ void prep_tile_bf16(PrepLds<true>& L, float* rec, int ti, int tj, int lane) {
+  const int fm = lane & 15, fq = lane >> 4;
+  const __bf16* ka = L.Kb + (16 * ti + fm) * kSB + 8 * fq;
+  const __bf16* qa = L.Qb + (16 * ti + fm) * kSB + 8 * fq;
+  const __bf16* kb = L.Kb + (16 * tj + fm) * kSB + 8 * fq;
+  f32x4v gacc = {0, 0, 0, 0}, qacc = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < kD / 32; ++s) {
+    const bf16x8 b8 = *(const bf16x8*)(kb + 32 * s);
+    if (DG) gacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8*)(ka + 32 * s), b8, gacc, 0, 0, 0);
+    if (DQ) qacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8*)(qa + 32 * s), b8, qacc, 0, 0, 0);
+  }
+  const float kfj = L.kf[16 * tj + fm];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = 16 * ti + 4 * fq + e;
+    if (DG) gacc[e] = gacc[e] * (L.betas[i] * L.kf[i]) * kfj;
+    if (DQ) qacc[e] = qacc[e] * L.qf[i] * kfj;
+  }
+  prep_tile_store<DG, DQ>(L, rec, ti, tj, lane, gacc, qacc);
+}
+
+// One 16x16 tile (ti, tj), tj <= ti, of G = (k beta) k^T (DG) and / or
+// QK = q k^T (DQ) on the normalised f32 rows.  The k-sum runs in the order
+// 16j + 4fq + e, so each lane reads its A and B operands as 16-byte vectors.
+template <bool DG, bool DQ, typename LT>
+__device__ __forceinline__ void prep_tile(LT& L, float* rec, int ti, int tj, int lane) {
   const int fm = lane & 15, fq = lane >> 4;
   const float* ka = L.Ks + (16 * ti + fm) * kSX + 4 * fq;
   const float* qa = L.Qs + (16 * ti + fm) * kSX + 4 * fq;
@@ -277,28 +343,15 @@ __device__ __forceinline__ void prep_tile(PrepLds& L, float* rec, int ti, int tj
       if (DQ) qacc = mma16(q4[e], b4[e], qacc);
     }
   }
-  const int j = 16 * tj + fm;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int i = 16 * ti + 4 * fq + e;
-    const float pair = j <= i ? expf(L.cums[i] - L.cums[j]) : 0.0f;
-    if (DG) L.Us[i * kSC + j] = j < i ? gacc[e] * pair : 0.0f;
-    if (DQ) L.In[i * kSC + j] = qacc[e] * pair;
-  }
-  if (DQ) {
-    wave_lds_sync();
-    f32x4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = L.In[(16 * ti + fm) * kSC + 16 * tj + 4 * e + fq];
-    *(f32x4*)(rec + kRecIn + 4 * ((ti * 4 + tj) * 64 + lane)) = v;
-  }
+  prep_tile_store<DG, DQ>(L, rec, ti, tj, lane, gacc, qacc);
 }
 
 // 16x16 diagonal block b of inv = (I + L)^-1, L = Us strict lower, by
 // forward substitution: lane j (of each 16-lane group) owns column j,
 //   inv[i][j] = -sum_{k<i} L[i][k] inv[k][j]  (inv[k][j] = 0 for k < j,
 //   1 for k == j); the L[i][k] reads are broadcasts.  Lanes with fq == 0 write.
-__device__ __forceinline__ void prep_inv16(PrepLds& L, int b, int lane) {
+template <typename LT>
+__device__ __forceinline__ void prep_inv16(LT& L, int b, int lane) {
   const int b0 = 16 * b, j = lane & 15;
   float col[16];
 #pragma unroll
@@ -329,7 +382,8 @@ __device__ __forceinline__ void prep_inv16(PrepLds& L, int b, int lane) {
 //   nv/kc  wave w: column tile w of new_values and k_cumdecay, row tiles 0-3
 template <typename T>
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
-  __shared__ PrepLds L;
+  constexpr bool BF = std::is_same<T, __bf16>::value;
+  __shared__ PrepLds<BF> L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fm = lane & 15, fq = lane >> 4;  // fragment row / k-slot of this lane
   const int c = blockIdx.x % g.n_chunks;
@@ -397,6 +451,20 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
         *(f32x4*)(qrow + 4 * hf) = a;
         *(f32x4*)(krow + 4 * hf) = b;
       }
+      if constexpr (BF) {
+        bf16x8 qb, kb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          qb[e] = (__bf16)qv[u][e];  // exact: the values came from bf16
+          kb[e] = (__bf16)kv[u][e];
+        }
+        *(bf16x8*)(L.Qb + (i0 + 32 * u) * kSB + col) = qb;
+        *(bf16x8*)(L.Kb + (i0 + 32 * u) * kSB + col) = kb;
+        if ((tid & 15) == 0) {
+          L.qf[i0 + 32 * u] = qscale / nq;
+          L.kf[i0 + 32 * u] = 1.0f / nk;
+        }
+      }
     }
   }
   // ---- gates (lane = chunk row): beta = sigmoid(b), g = softplus(a +
@@ -441,16 +509,25 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   // ---- G / QK tiles and the 16x16 diagonal inverses
   // (Tile indices by arithmetic: a table indexed by wave would be a global
   // load, and its wait would also wait for this wave's record stores.)
+  auto tile = [&](auto dg_c, auto dq_c, int ti, int tj) {
+    constexpr bool DG = decltype(dg_c)::value, DQ = decltype(dq_c)::value;
+    if constexpr (BF)
+      prep_tile_bf16<DG, DQ>(L, rec, ti, tj, lane);
+    else
+      prep_tile<DG, DQ>(L, rec, ti, tj, lane);
+  };
+  using Yes = std::true_type;
+  using No = std::false_type;
   if (wave < 3) {
     // wave 0: (1,0) (2,0); wave 1: (2,1) (3,0); wave 2: (3,1) (3,2)
-    prep_tile<true, true>(L, rec, wave == 0 ? 1 : wave + 1, wave == 0 ? 0 : 1, lane);
-    prep_tile<true, true>(L, rec, wave == 0 ? 2 : 3, wave == 2 ? 2 : 0, lane);
+    tile(Yes{}, Yes{}, wave == 0 ? 1 : wave + 1, wave == 0 ? 0 : 1);
+    tile(Yes{}, Yes{}, wave == 0 ? 2 : 3, wave == 2 ? 2 : 0);
   } else if (wave == 3) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) prep_tile<false, true>(L, rec, b, b, lane);
+    for (int b = 0; b < 4; ++b) tile(No{}, Yes{}, b, b);
   } else {
     const int b = wave - 4;
-    prep_tile<true, false>(L, rec, b, b, lane);
+    tile(Yes{}, No{}, b, b);
     wave_lds_sync();
     prep_inv16(L, b, lane);
   }
