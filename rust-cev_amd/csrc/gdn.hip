@@ -242,8 +242,18 @@ __device__ __forceinline__ float row16_sum(float x) {
 }
 
 constexpr int kSB = 136;  // LDS row stride (bf16 elements) of the raw 128-wide q / k rows
+constexpr int kST = 20;   // row stride (floats) of a packed 16x16 tile
 
-struct __attribute__((aligned(16))) PrepLdsBase {
+// Every access to ut and the inverse falls in a 16x16 tile at or below the
+// diagonal.  us(i, j) / iv(i, j) name element (i, j) of ut / inv.
+struct PrepGates {
+  float betas[kC], cums[kC], ecum[kC], ekd[kC];
+};
+template <bool BF>
+struct PrepLds;
+// f32 models: normalised f32 q / k rows, full 64 x 64 ut and inverse.
+template <>
+struct __attribute__((aligned(16))) PrepLds<false> : PrepGates {
   float Qs[kC * kSX];  // q normalised * dk^-0.5; later k_cumdecay staging
   float Ks[kC * kSX];  // k normalised
   float Us[kC * kSC];  // ut, strict lower (tiles at and below the diagonal)
@@ -251,19 +261,32 @@ struct __attribute__((aligned(16))) PrepLdsBase {
   // Products of the block inversion.  Before the inversion (the tile phase)
   // the same space holds the intra tiles on their way to record order.
   float Tm[kC * kSC];
-  float betas[kC], cums[kC], ecum[kC], ekd[kC];
+  __device__ float& us(int i, int j) { return Us[i * kSC + j]; }
+  __device__ float& iv(int i, int j) { return Iv[i * kSC + j]; }
+  __device__ float* kc_stage() { return Qs; }
 };
-// bf16 models also keep the raw q / k rows (the conv output, exact in bf16)
-// for the tile products, with each row's l2norm factor.
-template <bool BF>
-struct PrepLds : PrepLdsBase {};
+// bf16 models: the raw q / k rows (the conv output, exact in bf16) with each
+// row's l2norm factor, ut and the inverse packed as their ten lower 16x16
+// tiles; 78 KB, so two workgroups share a CU.
+constexpr int lower_tile(int ti, int tj) { return ti * (ti + 1) / 2 + tj; }
 template <>
-struct __attribute__((aligned(16))) PrepLds<true> : PrepLdsBase {
+struct __attribute__((aligned(16))) PrepLds<true> : PrepGates {
+  // Qb then Kb; after the inversion both hold the k_cumdecay staging
+  // (64 x kSX floats fit in their 64 x 2 kSB bf16).
   __bf16 Qb[kC * kSB];
   __bf16 Kb[kC * kSB];
+  float Us[10 * 16 * kST];
+  float Iv[10 * 16 * kST];
+  float Tm[kC * kSC];
   float qf[kC];  // dk^-0.5 / |q_i|
   float kf[kC];  // 1 / |k_i|
+  __device__ static int at(int i, int j) { return lower_tile(i >> 4, j >> 4) * (16 * kST) + (i & 15) * kST + (j & 15); }
+  __device__ float& us(int i, int j) { return Us[at(i, j)]; }
+  __device__ float& iv(int i, int j) { return Iv[at(i, j)]; }
+  __device__ float* kc_stage() { return (float*)Qb; }
 };
+static_assert(sizeof(PrepLds<true>) <= 80 * 1024, "two bf16 prep workgroups per CU");
+static_assert(kC * kSX * sizeof(float) <= 2 * kC * kSB * sizeof(__bf16), "k_cumdecay staging fits in Qb / Kb");
 
 // Epilogue of one 16x16 tile (ti, tj), tj <= ti, in the MFMA accumulator
 // layout (lane: column 16 tj + fm, rows 16 ti + 4 fq + e):
@@ -278,7 +301,7 @@ __device__ __forceinline__ void prep_tile_store(LT& L, float* rec, int ti, int t
   for (int e = 0; e < 4; ++e) {
     const int i = 16 * ti + 4 * fq + e;
     const float pair = j <= i ? expf(L.cums[i] - L.cums[j]) : 0.0f;
-    if (DG) L.Us[i * kSC + j] = j < i ? gacc[e] * pair : 0.0f;
+    if (DG) L.us(i, j) = j < i ? gacc[e] * pair : 0.0f;
     if (DQ) L.Tm[i * kSC + j] = qacc[e] * pair;
   }
   if (DQ) {
@@ -358,15 +381,14 @@ __device__ __forceinline__ void prep_inv16(LT& L, int b, int lane) {
   for (int k = 0; k < 16; ++k) col[k] = k == j ? 1.0f : 0.0f;
 #pragma unroll
   for (int i = 1; i < 16; ++i) {
-    const float* Lrow = L.Us + (b0 + i) * kSC + b0;
     float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < i; ++k) acc += Lrow[k] * col[k];
+    for (int k = 0; k < i; ++k) acc += L.us(b0 + i, b0 + k) * col[k];
     col[i] = i > j ? -acc : col[i];
   }
   if (lane < 16) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) L.Iv[(b0 + i) * kSC + b0 + j] = col[i];
+    for (int i = 0; i < 16; ++i) L.iv(b0 + i, b0 + j) = col[i];
   }
 }
 
@@ -438,20 +460,21 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
         sk += kv[u][e] * kv[u][e];
       }
       const float nq = sqrtf(row16_sum(sq) + 1e-6f), nk = sqrtf(row16_sum(sk) + 1e-6f);
-      float* qrow = L.Qs + (i0 + 32 * u) * kSX + col;
-      float* krow = L.Ks + (i0 + 32 * u) * kSX + col;
+      if constexpr (!BF) {
+        float* qrow = L.Qs + (i0 + 32 * u) * kSX + col;
+        float* krow = L.Ks + (i0 + 32 * u) * kSX + col;
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        f32x4 a, b;
+        for (int hf = 0; hf < 2; ++hf) {
+          f32x4 a, b;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          a[e] = qv[u][4 * hf + e] / nq * qscale;
-          b[e] = kv[u][4 * hf + e] / nk;
+          for (int e = 0; e < 4; ++e) {
+            a[e] = qv[u][4 * hf + e] / nq * qscale;
+            b[e] = kv[u][4 * hf + e] / nk;
+          }
+          *(f32x4*)(qrow + 4 * hf) = a;
+          *(f32x4*)(krow + 4 * hf) = b;
         }
-        *(f32x4*)(qrow + 4 * hf) = a;
-        *(f32x4*)(krow + 4 * hf) = b;
-      }
-      if constexpr (BF) {
+      } else {
         bf16x8 qb, kb;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -533,6 +556,20 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   }
   __syncthreads();
 
+  // Normalised q (times dk^-0.5) and k: stored in f32 for f32 models, the
+  // raw bf16 value times the row's factor for bf16 models.
+  auto q_hat = [&](int i, int c) {
+    if constexpr (BF)
+      return (float)L.Qb[i * kSB + c] * L.qf[i];
+    else
+      return L.Qs[i * kSX + c];
+  };
+  auto k_hat = [&](int i, int c) {
+    if constexpr (BF)
+      return (float)L.Kb[i * kSB + c] * L.kf[i];
+    else
+      return L.Ks[i * kSX + c];
+  };
   // Records the inversion's idle waves write: q e^cum (Qd) and k e^(last -
   // cum) (Kd) in their fragment orders, and intra's six zero tiles.
   auto qd_records = [&](int p0, int step) {
@@ -542,7 +579,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 16 * w + (l & 15), k = 4 * (4 * j + e) + (l >> 4);
-        v[e] = L.Qs[i * kSX + k] * L.ecum[i];
+        v[e] = q_hat(i, k) * L.ecum[i];
       }
       *(f32x4*)(rec + kRecQd + 4 * p) = v;
     }
@@ -554,7 +591,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 4 * (4 * jj + e) + (l >> 4), col = 16 * ti + (l & 15);
-        u[e] = L.Ks[i * kSX + col] * L.ekd[i];
+        u[e] = k_hat(i, col) * L.ekd[i];
       }
       *(f32x4*)(rec + kRecKd + 4 * p) = u;
     }
@@ -577,7 +614,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 16 * jg + 4 * fq + e;
-        kreg[4 * jg + e] = (L.Ks[i * kSX + 16 * wave + fm] * b4[e]) * e4[e];
+        kreg[4 * jg + e] = (k_hat(i, 16 * wave + fm) * b4[e]) * e4[e];
       }
     }
   };
@@ -587,20 +624,17 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   // inv_unit_lower, qwen35.rs:277-296)
   if (wave < 2) {
     const int o = 32 * wave;
-    const float* Ainv = L.Iv + o * kSC + o;
-    const float* Binv = L.Iv + (o + 16) * kSC + o + 16;
-    const float* Cb = L.Us + (o + 16) * kSC + o;
     f32x4v bc = {0, 0, 0, 0};
 #pragma unroll
-    for (int k = 0; k < 16; k += 4) bc = mma16(Binv[fm * kSC + k + fq], Cb[(k + fq) * kSC + fm], bc);
+    for (int k = 0; k < 16; k += 4) bc = mma16(L.iv(o + 16 + fm, o + 16 + k + fq), L.us(o + 16 + k + fq, o + fm), bc);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.Tm[(o + 4 * fq + e) * kSC + fm] = bc[e];
     wave_lds_sync();
     f32x4v x = {0, 0, 0, 0};
 #pragma unroll
-    for (int k = 0; k < 16; k += 4) x = mma16(L.Tm[(o + fm) * kSC + k + fq], Ainv[(k + fq) * kSC + fm], x);
+    for (int k = 0; k < 16; k += 4) x = mma16(L.Tm[(o + fm) * kSC + k + fq], L.iv(o + k + fq, o + fm), x);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) L.Iv[(o + 16 + 4 * fq + e) * kSC + o + fm] = -x[e];
+    for (int e = 0; e < 4; ++e) L.iv(o + 16 + 4 * fq + e, o + fm) = -x[e];
   } else {
     qd_records(tid - 128, 384);
   }
@@ -615,7 +649,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   if (wave < 4) {
     f32x4v bc = {0, 0, 0, 0};
     for (int k = 0; k < 16 * (ti2 + 1); k += 4)
-      bc = mma16(L.Iv[(32 + 16 * ti2 + fm) * kSC + 32 + k + fq], L.Us[(32 + k + fq) * kSC + 16 * tj2 + fm], bc);
+      bc = mma16(L.iv(32 + 16 * ti2 + fm, 32 + k + fq), L.us(32 + k + fq, 16 * tj2 + fm), bc);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.Tm[(16 * ti2 + 4 * fq + e) * kSC + 16 * tj2 + fm] = bc[e];
   } else {
@@ -626,9 +660,9 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   if (wave < 4) {
     f32x4v x = {0, 0, 0, 0};
     for (int k = 16 * tj2; k < 32; k += 4)
-      x = mma16(L.Tm[(16 * ti2 + fm) * kSC + k + fq], L.Iv[(k + fq) * kSC + 16 * tj2 + fm], x);
+      x = mma16(L.Tm[(16 * ti2 + fm) * kSC + k + fq], L.iv(k + fq, 16 * tj2 + fm), x);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) L.Iv[(32 + 16 * ti2 + 4 * fq + e) * kSC + 16 * tj2 + fm] = -x[e];
+    for (int e = 0; e < 4; ++e) L.iv(32 + 16 * ti2 + 4 * fq + e, 16 * tj2 + fm) = -x[e];
   } else {
     kd_records(kC * kD / 8 + tid - 256, kC * kD / 4, 256);
   }
@@ -637,14 +671,15 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   // ---- new_values = inv (v beta), k_cumdecay = inv (k beta e^cum) for the
   // row tiles ti of this wave's column tile; inv is lower triangular, so
   // row tile ti sums over k < 16 (ti + 1).  new_values goes out in the
-  // scan's accumulator order; k_cumdecay through this wave's columns of Qs
-  // (free now) into A-fragment order.
+  // scan's accumulator order; k_cumdecay through this wave's columns of the
+  // staging area (Qs, or Qb / Kb for bf16; free now) into A-fragment order.
+  float* stage = L.kc_stage();
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
     f32x4v nv = {0, 0, 0, 0}, kc = {0, 0, 0, 0};
     f32x4 a4[4];  // the row tile's inv operands, read before its MFMAs
 #pragma unroll
-    for (int jg = 0; jg <= ti; ++jg) a4[jg] = *(const f32x4*)(L.Iv + (16 * ti + fm) * kSC + 16 * jg + 4 * fq);
+    for (int jg = 0; jg <= ti; ++jg) a4[jg] = *(const f32x4*)&L.iv(16 * ti + fm, 16 * jg + 4 * fq);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int jg = 0; jg <= ti; ++jg) {
@@ -656,14 +691,14 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
     }
     *(f32x4*)(rec + kRecNv + ((wave * 4 + ti) * 64 + lane) * 4) = f32x4{nv[0], nv[1], nv[2], nv[3]};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) L.Qs[(16 * ti + 4 * fq + e) * kSX + 16 * wave + fm] = kc[e];
+    for (int e = 0; e < 4; ++e) stage[(16 * ti + 4 * fq + e) * kSX + 16 * wave + fm] = kc[e];
   }
   wave_lds_sync();
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
     f32x4 v;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = L.Qs[(16 * ti + fm) * kSX + 16 * wave + 4 * e + fq];
+    for (int e = 0; e < 4; ++e) v[e] = stage[(16 * ti + fm) * kSX + 16 * wave + 4 * e + fq];
     *(f32x4*)(rec + kRecKc + 4 * ((ti * 8 + wave) * 64 + lane)) = v;
   }
 }
