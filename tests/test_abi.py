@@ -184,6 +184,79 @@ def test_layer_norm_and_swiglu_validation(cev):
     assert L.cev_swiglu(CEV_BF16, 0, 64, None, None, 0, None, 0, None) == 0
 
 
+def test_linear_gather_and_kv_store_validation(cev):
+    """cev_linear, cev_gather_rows and the v store of cev_qknorm_rope_kv
+    refuse bad dtypes, sizes, strides, null and misaligned buffers before
+    any launch; a product of more than 8 rows needs a cev_blas handle."""
+    L = _abi.lib()
+    buf = (C.c_uint8 * 8192)()
+    a = C.addressof(buf)
+    al = a + (-a) % 16
+    p = C.c_void_p(al)
+    odd = C.c_void_p(al + 2)
+    lin = lambda dt, odt, m, n, k, x, ldx, w, ldw, alpha, y, ldy, h=None: L.cev_linear(  # noqa: E731
+        h, dt, odt, m, n, k, x, ldx, w, ldw, alpha, y, ldy, None, 0, None)
+    assert lin(7, CEV_F32, 2, 4, 64, p, 64, p, 64, 1.0, p, 4) == CEV_ERR_UNSUPPORTED
+    assert lin(CEV_F32, CEV_BF16, 2, 4, 64, p, 64, p, 64, 1.0, p, 4) == CEV_ERR_UNSUPPORTED   # f32 in, bf16 out
+    assert lin(CEV_BF16, CEV_F32, -1, 4, 64, p, 64, p, 64, 1.0, p, 4) == CEV_ERR_INVALID
+    assert lin(CEV_BF16, CEV_F32, 2, 4, 60, p, 64, p, 64, 1.0, p, 4) == CEV_ERR_INVALID       # k not 8-element rows
+    assert lin(CEV_BF16, CEV_F32, 2, 4, 64, p, 64, p, 64, float("nan"), p, 4) == CEV_ERR_INVALID
+    assert lin(CEV_BF16, CEV_F32, 2, 4, 64, None, 64, p, 64, 1.0, p, 4) == CEV_ERR_INVALID
+    assert lin(CEV_BF16, CEV_F32, 2, 4, 64, p, 32, p, 64, 1.0, p, 4) == CEV_ERR_INVALID       # ldx < k
+    assert lin(CEV_BF16, CEV_F32, 2, 4, 64, p, 64, p, 64, 1.0, p, 2) == CEV_ERR_INVALID       # ldy < n
+    assert lin(CEV_BF16, CEV_F32, 2, 4, 64, odd, 64, p, 64, 1.0, p, 4) == CEV_ERR_INVALID
+    assert lin(CEV_BF16, CEV_F32, 16, 4, 64, p, 64, p, 64, 1.0, p, 4) == CEV_ERR_INVALID      # 16 rows, no handle
+    assert lin(CEV_BF16, CEV_F32, 0, 4, 64, None, 0, None, 0, 1.0, None, 0) == 0               # nothing to do
+    gat = lambda dt, odt, n, width, table, ldt, rows, ids, out, ldo: L.cev_gather_rows(  # noqa: E731
+        dt, odt, n, width, table, ldt, rows, ids, out, ldo, None)
+    assert gat(7, CEV_F32, 2, 8, p, 8, 4, None, p, 8) == CEV_ERR_UNSUPPORTED
+    assert gat(CEV_BF16, 9, 2, 8, p, 8, 4, None, p, 8) == CEV_ERR_UNSUPPORTED
+    assert gat(CEV_BF16, CEV_F32, -2, 8, p, 8, 4, None, p, 8) == CEV_ERR_INVALID
+    assert gat(CEV_BF16, CEV_F32, 2, 8, None, 8, 4, None, p, 8) == CEV_ERR_INVALID
+    assert gat(CEV_BF16, CEV_F32, 2, 8, p, 4, 4, None, p, 8) == CEV_ERR_INVALID                # ld_table < width
+    assert gat(CEV_BF16, CEV_F32, 6, 8, p, 8, 4, None, p, 8) == CEV_ERR_INVALID                # 6 rows of a 4-row table
+    assert gat(CEV_BF16, CEV_F32, 0, 8, None, 0, 0, None, None, 0) == 0
+    d = _abi.QkNormDesc()
+    assert L.cev_qknorm_desc_init(C.byref(d), CEV_BF16, 8, 2, 128, 4, 128, 10, 0, 1e-6, 0) == 0
+    pos = (C.c_int32 * 4)()
+    kv = lambda v_in, vi_t, v_out, vo_t: L.cev_qknorm_rope_kv(  # noqa: E731
+        C.byref(d), p, p, v_in, vi_t, 128, p, p, pos, p, p, None, 0, p, p, v_out, vo_t, 128, None)
+    assert kv(p, 256, None, 256) == CEV_ERR_INVALID       # v_in without v_out
+    assert kv(odd, 256, p, 256) == CEV_ERR_INVALID        # misaligned v rows
+    assert kv(p, 260, p, 256) == CEV_ERR_INVALID          # v row stride breaks 16-byte rows
+
+
+def test_prefix_store_argument_errors(cev):
+    """The store refuses empty reservations, unknown ranges and bad
+    capacities with CEV_ERR_INVALID, and a reservation beyond the capacity
+    with CEV_ERR_SPACE; a refused call changes nothing."""
+    L = _abi.lib()
+    h = C.c_void_p()
+    assert L.cev_prefix_store_create(0, 10, C.byref(h)) == CEV_ERR_INVALID
+    assert L.cev_prefix_store_create(10, -1, C.byref(h)) == CEV_ERR_INVALID
+    store = cev_hip.PrefixStore(capacity=64, budget=64)
+    for bad in (0, -3):
+        with pytest.raises(CevError) as e:
+            store.reserve(bad)
+        assert e.value.code == CEV_ERR_INVALID
+    with pytest.raises(CevError) as e:
+        store.reserve(65)
+    assert e.value.code == CEV_ERR_SPACE
+    b = store.reserve(16)
+    with pytest.raises(CevError) as e:
+        store.put(list(range(8)), b)       # length differs from the reservation
+    assert e.value.code == CEV_ERR_INVALID
+    with pytest.raises(CevError) as e:
+        store.release(b + 1)               # not the start of a held range
+    assert e.value.code == CEV_ERR_INVALID
+    assert store.stats()["used_slots"] == 16
+    store.release(b)
+    with pytest.raises(CevError) as e:
+        store.release(b)                   # already released
+    assert e.value.code == CEV_ERR_INVALID
+    assert store.stats() == {"entries": 0, "cached_tokens": 0, "used_slots": 0}
+
+
 # ---------------------------------------------------------------- table builders vs reference masks
 
 
