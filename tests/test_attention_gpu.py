@@ -378,6 +378,50 @@ def test_long_prefix_short_suffix_split(gpu, orc, blocks):
     assert np.abs(to_np(whole) - split).max() <= 4e-3
 
 
+def test_million_key_prefix_many_parts(gpu):
+    """A 2^20-key cached prefix (256 MiB of K per head) with one 16-token
+    causal block, g = 8: the planner cuts the single tile's key stream into
+    the most parts it allows, and the merge combines them over several
+    batches.  Sampled rows and heads are held to exact attention computed in
+    f64 over all 2^20 + 16 keys, and the split result to the unsplit one."""
+    import torch
+    P, t, hq, hkv, d = 1 << 20, 16, 8, 1, 128
+    _say(f"test 1M-key prefix: P={P} t={t} hq={hq} hkv={hkv}")
+    rng = np.random.default_rng(20)
+    f = lambda *shape: torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(gpu).to(torch.bfloat16)  # noqa: E731
+    q, kn, vn = f(t, hq, d), f(t, hkv, d), f(t, hkv, d)
+    kc, vc = f(hkv, P, d), f(hkv, P, d)
+    # Random keys alone give a near-uniform softmax over 2^20 keys and
+    # outputs near zero; a few planted keys aligned with each sampled query
+    # (at the start, the middle and the end of the prefix) carry most of its
+    # weight, so the outputs are O(1) and every part of the split matters.
+    samples = [(0, 0, (5, 524_301, P - 3)), (7, 3, (77_777, 600_000, P - 9)), (15, 7, (1, 300_000, 1_000_003))]
+    for i, h, where in samples:
+        for pos in where:
+            kc[0, pos] = (1.5 * q[i, h].float()).to(torch.bfloat16)
+    tab = cev_hip.BlockTable.from_rows(1, t, P, causal=True)
+    attn = cev_hip.PackedAttention(q, kn, tab, k_cache=kc, s_cache=P, v_new=vn, v_cache=vc)
+    assert attn.plan.n_splits >= 128, attn.plan.n_splits
+    out = to_np(attn(q, kn, vn, kc, vc))
+    whole = to_np(cev_hip.packed_attention(q, kn, vn, tab, k_cache=kc, v_cache=vc, max_splits=1))
+    assert np.isfinite(out).all()
+    # two bf16 ulps at the planted rows' magnitude (|out| < 2): the parts
+    # sum in another order than the single stream
+    assert np.abs(whole - out).max() <= 2 * 2.0 ** -7
+    k_all = np.concatenate([to_np(kc)[0], to_np(kn)[:, 0]]).astype(np.float64)
+    v_all = np.concatenate([to_np(vc)[0], to_np(vn)[:, 0]]).astype(np.float64)
+    qn = to_np(q).astype(np.float64)
+    worst = 0.0
+    for i, h, _ in samples:
+        keys = P + i + 1  # the prefix and the block's own keys up to row i
+        sc = k_all[:keys] @ qn[i, h] / np.sqrt(d)
+        pr = np.exp(sc - sc.max())
+        ref = (pr @ v_all[:keys]) / pr.sum()
+        worst = max(worst, float(np.abs(out[i, h] - ref).max()))
+    _say(f"  parts {attn.plan.n_splits}, max|d| vs exact f64 {worst:.3g}")
+    assert worst <= BF16_TOL
+
+
 def test_split_f32_matches_unsplit(gpu):
     w = configs.c1()
     gl = GpuLayer(w, gpu)
