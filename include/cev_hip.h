@@ -256,7 +256,7 @@ int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, const void* z,
                         void* conv_out, float* s_out, void* workspace, size_t workspace_bytes, cev_stream stream);
 
 /* ------------------------------------------------------------------ */
-/* Decoder-layer pieces around attention (Qwen3 stack, config-2 passes). */
+/* Decoder-layer pieces around attention (the Qwen3 decoder stack's packed passes). */
 
 /* RMSNorm of `rows` rows of `hidden` elements, candle_nn RmsNorm in the
  * model dtype (input_layernorm / post_attention_layernorm / final norm,

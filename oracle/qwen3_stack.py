@@ -173,7 +173,7 @@ def debias_scores(logits, order, span_begin, span_len, n_options, calib=None) ->
 
 
 def run_config(w, weights=None):
-    """The whole config-2 flow on the oracle: prefill the head, one packed
+    """The whole Qwen3-1.7B-shaped packed-pass flow on the oracle: prefill the head, one packed
     pass (tail + questions), code-head probabilities.  Returns
     (probabilities (questions, n_codes) f64, hidden (questions, H) f32)."""
     weights = w.weights() if weights is None else weights

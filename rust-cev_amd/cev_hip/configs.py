@@ -174,7 +174,7 @@ WORKLOADS = {"c1": c1, "c3": c3, "c4": c4, "c5a": c5_attention, "hbm": hbm}
 
 @dataclass
 class GdnWorkload:
-    """One Gated DeltaNet layer of a Qwen3.5 hybrid prefix (config 5's GDN
+    """One Gated DeltaNet layer of a Qwen3.5 hybrid prefix (the 4096-token prefix's GDN
     part: Hk = 16 repeated to Hv = 32, dk = dv = 128, conv kernel 4, 64-token
     chunks).  Synthetic inputs stand for the projection outputs: q/k/v/z
     N(0,1); beta = sigmoid(b) uniform in (0, 1) and the per-token decay

@@ -76,7 +76,7 @@ CEV_HD static inline int64_t cev_attn_partial_floats(int head_dim) { return (int
 // stream into parts of fewer than kSplitMinChunks chunks (kSplitMinChunksF32
 // for f32, whose 32-key chunk is about eight times the work of a bf16
 // 64-key chunk).  Measured: the 32k-prefix x 16-token shape (8 tile x head
-// items) 32 parts 38 us, 64 parts 49 us; the config-2 pass's attention (224
+// items) 32 parts 38 us, 64 parts 49 us; the 28-layer Qwen3-1.7B-shaped pass's attention (224
 // items) unsplit 86.7 us, 2 parts 119.8 us; the f32 12 x 32-token shape
 // after a 256-token prefix (24 items of 12 chunks) 3 parts 50 us, 6 parts
 // 38 us, 10 parts 39 us; 512 workgroups (two rounds) were slower on every

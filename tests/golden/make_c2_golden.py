@@ -1,5 +1,5 @@
 """Writes tests/golden/c2_f32.npz and c2_bf16.npz: the oracle's answer-code
-probabilities and final hidden state for config 2 in f32 and in bf16 (28
+probabilities and final hidden state of the 28-layer Qwen3-1.7B-shaped pass in f32 and in bf16 (28
 layers, full vocab), the fixtures test_qwen3_stack_gpu.py compares the
 device stack with.
 
@@ -29,7 +29,7 @@ def main(dtypes):
         weights = w.weights()
         print(f"weights: {time.time() - t0:.1f} s", flush=True)
         p, hid = qwen3_stack.run_config(w, weights)
-        print(f"oracle config 2 ({dt}): {time.time() - t0:.1f} s; p[0] = {np.round(p[0], 5)}", flush=True)
+        print(f"oracle 28-layer pass ({dt}): {time.time() - t0:.1f} s; p[0] = {np.round(p[0], 5)}", flush=True)
         np.savez_compressed(os.path.join(HERE, f"c2_{dt}.npz"), p=p, hidden=hid.astype(np.float32))
 
 

@@ -1,7 +1,7 @@
-"""Writes tests/golden/c2_hf_f32.npz: config 2's answer-code probabilities
+"""Writes tests/golden/c2_hf_f32.npz: the Qwen3-1.7B-shaped stack's answer-code probabilities
 and final hidden states from HF transformers' Qwen3ForCausalLM, the model
 the reference pins its f32 path against (README.md:48, |dp| < 5e-5), on the
-config-2 seeded weights at 2 layers and a 4096-token vocab.
+seeded weights of that stack at 2 layers and a 4096-token vocab.
 
 Each question is asked alone over [state || question]: the 2048-token state
 runs once, and every question continues from a copy of its KV cache with

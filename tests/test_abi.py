@@ -380,7 +380,7 @@ def test_split_policy(cev):
     d = cev_hip.attn_desc(CEV_BF16, 32, 8, 128, 16, 32768)
     assert cev_hip.AttnPlan(d, hbm).n_splits == 32
     # 224 workgroups already fill the round: splitting would add a second
-    # round and the merge (the config-2 pass)
+    # round and the merge (the 28-layer Qwen3-1.7B-shaped pass)
     tab, _, _ = cev_hip.BlockTable.from_plans([(1536, 2048, 1536)], [(0, 48)] * 64)
     d = cev_hip.attn_desc(CEV_BF16, 16, 8, 128, tab.t, tab.s_cache)
     p = cev_hip.AttnPlan(d, tab)

@@ -6,7 +6,7 @@ Bars: the chunk rule is f32 in the reference and is checked to 1e-4 max |d|
 (the reference's own chunked-vs-recurrence test allows 2e-4,
 qwen35.rs:776-822; the GPU sums in another order).  In bf16 the layer output
 is cast to bf16 once at the end and is checked to the 2e-2 bf16 bar; the new
-conv state is a copy and must match bit for bit.  At the config-5 size the
+conv state is a copy and must match bit for bit.  At the 4096-token size the
 oracle runs on a prefix of the sequence, and the split-sequence property
 (T1 then T2 with the carried states == T1 + T2 at once) covers the rest.
 """
@@ -140,7 +140,7 @@ def test_gdn_c5_heads_vs_oracle(gpu, orc):
 
 def test_gdn_c5_split_sequence(gpu):
     """4096 tokens at once == 2048 + 2048 with the carried conv and recurrent
-    state (size-independent continuation property at the full config-5 size)."""
+    state (size-independent continuation property at the full 4096-token, 32-head size)."""
     w = configs.c5_gdn()
     inp = w.inputs()
     _say(f"test gdn c5 split: T={w.t}")
@@ -163,7 +163,7 @@ def test_gdn_long_sequence_split(gpu):
     workspace, 32,768 prep workgroups) == the same tokens in two halves with
     the carried conv and recurrent state.  The halves meet at a chunk
     boundary, so every chunk is computed the same way in both runs.  Inputs
-    are drawn on the device with config 5's distributions (beta uniform in
+    are drawn on the device with the 4096-token workload's distributions (beta uniform in
     (0, 1), decay e^g log-uniform in [1e-3, 1])."""
     import torch
     T, nk, nv, d, K = 1 << 16, 16, 32, 128, 4

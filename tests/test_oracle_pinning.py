@@ -660,7 +660,7 @@ def test_c2_oracle_matches_hf_transformers(orc):
     placement, QK-norm + RoPE, the engine's chunked head prefill and packed
     pass, final norm at the gather rows, tied code head) against
     Qwen3ForCausalLM asked each question alone over [state || question], on
-    config 2's seeded weights at 2 layers: the reference's own pin of its
+    the Qwen3-1.7B-shaped stack's seeded weights at 2 layers: the reference's own pin of its
     f32 path (README.md:48, |dp| < 5e-5)."""
     from cev_hip import configs
     from oracle.engine import OracleEngine

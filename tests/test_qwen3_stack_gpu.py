@@ -47,7 +47,7 @@ def _gpu_engine(w, weights, device, budget=None, pass_tokens=None, capacity=None
 
 
 def _gpu_config(w, weights, device):
-    """The config-2 flow on the device through the engine (prefill of the
+    """The Qwen3-1.7B-shaped packed-pass flow on the device through the engine (prefill of the
     head into the prefix store's slots, one packed pass of the tail and the
     questions).  Returns (probabilities, hidden, engine)."""
     from cev_hip.qwen3 import softmax64
@@ -210,7 +210,7 @@ def test_engine_request_and_twin_then_eviction(gpu, orc):
 def test_stack_two_layers_vs_hf_transformers(gpu):
     """The device engine against HF transformers' Qwen3ForCausalLM asked
     each question alone over [state || question] (tests/golden/make_c2_hf.py),
-    config 2's widths at 2 layers, f32: the reference's own bar
+    the Qwen3-1.7B-shaped widths at 2 layers, f32: the reference's own bar
     (README.md:48)."""
     from cev_hip.qwen3 import softmax64
     g = np.load(HF_GOLDEN)
@@ -234,7 +234,7 @@ def test_config2_full_bf16_vs_golden(gpu):
     1.4 % at 2 layers, 4.6 % at 28)."""
     w = configs.c2(True)
     g = np.load(GOLDEN_BF16)
-    _say(f"test config 2 full bf16: layers={w.n_layers} vocab={w.vocab}")
+    _say(f"test 28-layer stack bf16: layers={w.n_layers} vocab={w.vocab}")
     p, hid, _ = _gpu_config(w, w.weights(), gpu)
     dp = float(np.abs(p - g["p"]).max())
     dh = float(np.abs(hid - g["hidden"]).max())
@@ -250,7 +250,7 @@ def test_config2_full_f32_vs_golden(gpu):
     oracle's fixture."""
     w = configs.c2(False)
     g = np.load(GOLDEN)
-    _say(f"test config 2 full: layers={w.n_layers} vocab={w.vocab} (weights {w.n_layers * 201 + 1245} MB f32)")
+    _say(f"test 28-layer stack f32: layers={w.n_layers} vocab={w.vocab} (weights {w.n_layers * 201 + 1245} MB f32)")
     p, hid, _ = _gpu_config(w, w.weights(), gpu)
     dp = float(np.abs(p - g["p"]).max())
     dh = float(np.abs(hid - g["hidden"]).max())
@@ -291,7 +291,7 @@ def _device_debias(gpu, logits, order, begin, length, ks, calib=None):
 @pytest.mark.parametrize("calibrated", [False, True])
 def test_debias_scores_match_oracle(gpu, calibrated):
     """cev_debias_scores against the oracle's restatement of
-    Service::run_debiased's averaging (service.rs:330-345): config 2's
+    Service::run_debiased's averaging (service.rs:330-345): the packed pass's
     16 questions x 4 rotations x 8 codes plus ragged option counts (1..64).
     f64 exp / log may differ by an ulp between libm and the device: the f32
     scores are held to 2 ulp-scale."""
