@@ -755,26 +755,25 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     f32x4 kc[4], qd[4], kd[4], in[2], nvv;
     float decay;
   };
-  auto fetch = [&](int c, Ops& o) {
-    const float* rec = g.rec + ((int64_t)item * g.n_chunks + c) * kRecFloats;
-    const f32x4* kcp = (const f32x4*)(rec + kRecKc) + rt * 8 * 64 + 4 * kh * 64 + lane;
-    const f32x4* qdp = (const f32x4*)(rec + kRecQd) + rt * 8 * 64 + 4 * kh * 64 + lane;
-    const f32x4* kdp = (const f32x4*)(rec + kRecKd) + wave * 4 * 64 + lane;
+  // this lane's float offsets inside a record: kc / qd operand j at + 256 j,
+  // kd operand j at + 256 j, intra blocks kh and kh + 2 at + 0 and + 512
+  const int kc_off = kRecKc + 4 * (rt * 8 * 64 + 4 * kh * 64 + lane);
+  const int qd_off = kRecQd + 4 * (rt * 8 * 64 + 4 * kh * 64 + lane);
+  const int kd_off = kRecKd + 4 * (wave * 4 * 64 + lane);
+  const int in_off = kRecIn + 4 * (rt * 4 * 64 + kh * 64 + lane);
+  const int nv_off = kRecNv + 4 * ((sl * 4 + rt) * 64 + lane);  // read by kh = 0 only
+  auto rec_at = [&](int c) { return g.rec + ((int64_t)item * g.n_chunks + c) * kRecFloats; };
+  auto ld4 = [](const float* p) { return *(const f32x4*)p; };
+  auto fetch = [&](const float* rec, Ops& o) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      o.kc[j] = kcp[j * 64];
-      o.qd[j] = qdp[j * 64];
-      o.kd[j] = kdp[j * 64];
+      o.kc[j] = ld4(rec + kc_off + 256 * j);
+      o.qd[j] = ld4(rec + qd_off + 256 * j);
+      o.kd[j] = ld4(rec + kd_off + 256 * j);
     }
-    // intra blocks j = kh, kh + 2 of row tile rt
-    const f32x4* inp = (const f32x4*)(rec + kRecIn) + rt * 4 * 64 + kh * 64 + lane;
-    o.in[0] = inp[0];
-    o.in[1] = inp[2 * 64];
-    if (kh == 0) {
-      o.nvv = *((const f32x4*)(rec + kRecNv) + (sl * 4 + rt) * 64 + lane);
-    } else {
-      o.nvv = f32x4{};
-    }
+    o.in[0] = ld4(rec + in_off);
+    o.in[1] = ld4(rec + in_off + 512);
+    o.nvv = ld4(rec + nv_off);
     o.decay = rec[kRecDecay];
   };
   // the output of the previous chunk (kh = 0 waves): its first half and intra
@@ -782,15 +781,26 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
   f32x4v out_prev = {0, 0, 0, 0};
   auto store_out = [&](int c) {
     if (kh == 0 && c >= 0) {
+      // the four Opart reads go out together, ahead of the stores' branches
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = out_prev[e] + Opart[(16 * rt + 4 * fq + e) * 20 + fm];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int row = 16 * rt + 4 * fq + e;
-        const int t = c * kC + row;
-        if (t < g.t) g.core[(((int64_t)r * g.t + t) * g.nv + h) * kD + col0 + fm] = out_prev[e] + Opart[row * 20 + fm];
+        const int t = c * kC + 16 * rt + 4 * fq + e;
+        if (t < g.t) g.core[(((int64_t)r * g.t + t) * g.nv + h) * kD + col0 + fm] = o[e];
       }
     }
   };
-  auto chunk = [&](int c, Ops& cur, Ops& nxt) {
+  // One chunk.  With kPrefetch the next chunk's operands (nrec) load into
+  // nxt one phase ahead of their use, a few loads after each group of four
+  // MFMAs: phase A loads the next phase A's k_cumdecay, new_values and decay,
+  // phase B the next phase B's operands.  Each wave issues 15 16-byte loads
+  // per chunk and the CU's load path takes 64 B/clk, so a burst of them
+  // would hold every wave's next instruction (and the barrier after it) for
+  // about 1.8k cycles; spread out, they issue while the MFMAs run and each
+  // has a whole chunk to land.
+  auto chunk = [&](int c, Ops& cur, Ops& nxt, const float* nrec) {
     store_out(c - 1);
     // phase A: this wave's half of dk against the state slice; the 16 state
     // operands are read before the first MFMA and reused by (q e^cum) . S
@@ -800,9 +810,19 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     __builtin_amdgcn_sched_barrier(0);
     f32x4v acc = {0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc = mma16(cur.kc[j][e], sb[4 * j + e], acc);
+      if (kPrefetch) {
+        __builtin_amdgcn_sched_barrier(0);
+        nxt.kc[j] = ld4(nrec + kc_off + 256 * j);
+        if (j == 3) {
+          nxt.nvv = ld4(nrec + nv_off);
+          nxt.decay = nrec[kRecDecay];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = 16 * rt + 4 * fq + e;
@@ -811,12 +831,6 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
       else
         Vn1[row * 20 + fm] = acc[e];
     }
-    // The next chunk's operands (about 139 KB per workgroup through the
-    // CU's 64 B/clk load path) are issued after this phase's MFMAs, which
-    // would otherwise queue behind them, and land during phase B.
-    // Unconditional (the last chunk fetches itself again): a branch around
-    // the loads made the compiler's wait tracking give up at the join.
-    if (kPrefetch) fetch(min(c + 1, g.n_chunks - 1), nxt);
     __syncthreads();
     // phase B
     float vb[16];
@@ -825,12 +839,20 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     __builtin_amdgcn_sched_barrier(0);
     f32x4v su = {0, 0, 0, 0}, ob = {0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         su = mma16(cur.kd[j][e], vb[4 * j + e], su);
         ob = mma16(cur.qd[j][e], sb[4 * j + e], ob);
       }
+      if (kPrefetch) {
+        __builtin_amdgcn_sched_barrier(0);
+        nxt.qd[j] = ld4(nrec + qd_off + 256 * j);
+        nxt.kd[j] = ld4(nrec + kd_off + 256 * j);
+        if (j < 2) nxt.in[j] = ld4(nrec + in_off + 512 * j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     // intra . v_new: intra is lower triangular (K stops at the diagonal
     // block); blocks j = kh, kh + 2 go to this wave so the two halves share it
     // (kh picks the path: a register array indexed by it would live in scratch)
@@ -863,22 +885,23 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     __syncthreads();
   };
   Ops ops_a, ops_b;
-  fetch(0, ops_a);
+  fetch(rec_at(0), ops_a);
   if constexpr (kPrefetch) {
-    // One chunk per iteration: chunk c+1's operands load into ops_b while c
-    // computes, then move to ops_a.
-    for (int c = 0; c < g.n_chunks; ++c) {
-      chunk(c, ops_a, ops_b);
-      // s_waitcnt vmcnt(0): the prefetch has had the whole chunk to land;
-      // with nothing pending at the loop head the compiler no longer waits
-      // for the next prefetch before the first MFMA of the next chunk
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      ops_a = ops_b;
+    // Two chunks per iteration so the operand sets alternate without a copy
+    // (a copy would wait for every prefetch to land).  The prefetch address
+    // is clamped to the last chunk: the loads stay unconditional, because a
+    // branch around them made the compiler's wait tracking give up.
+    const int last = g.n_chunks - 1;
+    int c = 0;
+    for (; c + 1 < g.n_chunks; c += 2) {
+      chunk(c, ops_a, ops_b, rec_at(c + 1));
+      chunk(c + 1, ops_b, ops_a, rec_at(min(c + 2, last)));
     }
+    if (c < g.n_chunks) chunk(c, ops_a, ops_b, rec_at(last));
   } else {
     for (int c = 0; c < g.n_chunks; ++c) {
-      if (c > 0) fetch(c, ops_a);
-      chunk(c, ops_a, ops_a);
+      if (c > 0) fetch(rec_at(c), ops_a);
+      chunk(c, ops_a, ops_a, nullptr);
     }
   }
   store_out(g.n_chunks - 1);
