@@ -99,8 +99,43 @@ struct GdnArgs {
 // weights stay in registers and the last K-1 input rows slide through a
 // register window, so every input row is read once as one 16-byte vector.
 // Each product and partial sum is one model-dtype op (decoder.rs:143-150);
-// SiLU is candle's v / (1 + exp(-v)) with each op in the model dtype.
+// SiLU is candle's v / (1 + exp(-v)) with each op in the model dtype.  The
+// thread of a row's last run also writes the new conv state: its window then
+// holds the last K-1 columns of [state || x] (qwen35.rs:429).
 constexpr int kConvRun = 16;
+// 16 waves per workgroup share one table; widths 7 and 8 need more than the
+// 128 registers that leaves each lane, so they run 8 waves
+constexpr int conv_threads(int K) { return K <= 6 ? 1024 : 512; }
+
+// The bf16 SiLU of a bf16 value depends on its 16 bits only.  Each conv
+// workgroup first tabulates it in LDS for |v| in [2^-16, 2^7) (23 binades of
+// 128 mantissas per sign), evaluated by the same silu_bf16 below, so a table
+// hit is bit-identical to evaluating it.  A token whose 8 x 64 values are not
+// all in that range takes silu_bf16 itself (wave-uniform branch).
+constexpr uint32_t kSiluLo = (127 - 16) * 128;  // |bits| of 2^-16
+constexpr uint32_t kSiluSpan = 23 * 128;        // entries per sign
+constexpr int kSiluEntries = 2 * (int)kSiluSpan;
+
+__device__ __forceinline__ float silu_bf16(float v) {
+  const float ex = bf16_round(expf(-v));
+  const float den = bf16_round(1.0f + ex);
+  return bf16_round(v / den);
+}
+
+// table slot of a bf16-exact value: negative values after the positive ones;
+// >= kSiluEntries when |v| is outside the table
+__device__ __forceinline__ uint32_t silu_slot(float v) {
+  const uint32_t b = __float_as_uint(v) >> 16;
+  const uint32_t m = (b & 0x7fffu) - kSiluLo;
+  return m < kSiluSpan ? m + (b >> 15) * kSiluSpan : (uint32_t)kSiluEntries;
+}
+
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+// two values rounded to bf16 by one conversion
+__device__ __forceinline__ f32x2v bf16_round2(f32x2v x) {
+  return __builtin_convertvector(__builtin_convertvector(x, bf16x2v), f32x2v);
+}
 
 template <typename T>
 __device__ __forceinline__ void load8(const T* p, float* v);
@@ -119,6 +154,26 @@ __device__ __forceinline__ void load8<float>(const float* p, float* v) {
     v[e + 4] = y[e];
   }
 }
+// 8 channels of one input row as loaded (converted to f32 where used, so a
+// row loaded one iteration ahead is not waited for early)
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<__bf16> {
+  bf16x8 x;
+  __device__ __forceinline__ void load(const __bf16* p) { x = *(const bf16x8*)p; }
+  __device__ __forceinline__ float operator[](int e) const { return (float)x[e]; }
+};
+template <>
+struct Raw8<float> {
+  f32x4 x, y;
+  __device__ __forceinline__ void load(const float* p) {
+    x = *(const f32x4*)p;
+    y = *(const f32x4*)(p + 4);
+  }
+  __device__ __forceinline__ float operator[](int e) const { return e < 4 ? x[e] : y[e - 4]; }
+};
+
 template <typename T>
 __device__ __forceinline__ void store8(T* p, const float* v);
 template <>
@@ -135,7 +190,7 @@ __device__ __forceinline__ void store8<float>(float* p, const float* v) {
 }
 
 template <typename T, int K>
-__device__ __forceinline__ void conv_run(const GdnArgs& g, int r, int t0, int c0) {
+__device__ __forceinline__ void conv_run(const GdnArgs& g, const float* silu_tab, int r, int t0, int c0) {
   const T* x = (const T*)g.mixed + r * g.mixed_sb;
   const T* tail = g.conv_in ? (const T*)g.conv_in + r * g.conv_in_sb : nullptr;
   float w[8][K];
@@ -157,22 +212,51 @@ __device__ __forceinline__ void conv_run(const GdnArgs& g, int r, int t0, int c0
   }
   T* out = (T*)g.conved + ((int64_t)r * g.t + t0) * g.conv_dim + c0;
   const int n = min(kConvRun, g.t - t0);
+  // the next row loads while this one is computed (the last load repeats
+  // the last row, so it stays unconditional and in bounds)
+  Raw8<T> next;
+  const T* xp = x + (int64_t)t0 * g.mixed_st + c0;
+  next.load(xp);
+  // s_waitcnt vmcnt(0): with nothing pending at the loop entry, the wait at
+  // the loop head covers only the prefetch, not the previous row's store
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   for (int i = 0; i < n; ++i) {
-    load8<T>(x + (int64_t)(t0 + i) * g.mixed_st + c0, win[K - 1]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) win[K - 1][e] = next[e];
+    xp += i + 1 < n ? g.mixed_st : 0;
+    next.load(xp);
     float y[8];
+    if constexpr (sizeof(T) == 2) {
+      // products and partial sums, each rounded to bf16, two channels per
+      // conversion
+      f32x2v acc[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float acc = 0.0f;
+      for (int u = 0; u < K; ++u)
 #pragma unroll
-      for (int u = 0; u < K; ++u) {
-        const float term = rnd<T>(win[u][e] * w[e][u]);
-        acc = u == 0 ? term : rnd<T>(acc + term);
+        for (int q = 0; q < 4; ++q) {
+          const f32x2v term = bf16_round2(f32x2v{win[u][2 * q] * w[2 * q][u], win[u][2 * q + 1] * w[2 * q + 1][u]});
+          acc[q] = u == 0 ? term : bf16_round2(acc[q] + term);
+        }
+      uint32_t slot[8];
+      bool hit = true;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        slot[e] = silu_slot(acc[e / 2][e % 2]);
+        hit = hit && slot[e] < (uint32_t)kSiluEntries;
       }
-      if (sizeof(T) == 2) {
-        const float ex = bf16_round(expf(-acc));
-        const float den = bf16_round(1.0f + ex);
-        y[e] = bf16_round(acc / den);
+      if (__all(hit)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = silu_tab[slot[e]];
       } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = silu_bf16(acc[e / 2][e % 2]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < K; ++u) acc = u == 0 ? win[u][e] * w[e][u] : acc + win[u][e] * w[e][u];
         y[e] = acc / (1.0f + expf(-acc));
       }
     }
@@ -182,46 +266,56 @@ __device__ __forceinline__ void conv_run(const GdnArgs& g, int r, int t0, int c0
 #pragma unroll
       for (int e = 0; e < 8; ++e) win[j][e] = win[j + 1][e];
   }
+  if (t0 + n == g.t) {
+    // new conv state (conv_dim, K-1) of this row: the window's last K-1 columns
+    T* st = (T*)g.conv_out + ((int64_t)r * g.conv_dim + c0) * (K - 1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int j = 0; j < K - 1; ++j) st[e * (K - 1) + j] = from_f<T>(win[j][e]);
+  }
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void gdn_conv_kernel(GdnArgs g) {
+// One kernel per conv width, so each gets its own register allocation (the
+// window and weights take 16 K registers).
+template <typename T, int K>
+__global__ __launch_bounds__(conv_threads(K)) void gdn_conv_kernel(GdnArgs g) {
+  constexpr int kConvThreads = conv_threads(K);
+  __shared__ float silu_tab[sizeof(T) == 2 ? kSiluEntries : 1];
+  if constexpr (sizeof(T) == 2) {
+    for (int i = threadIdx.x; i < kSiluEntries; i += kConvThreads) {
+      const uint32_t neg = i >= (int)kSiluSpan;
+      const uint32_t bits = (neg << 15) | (kSiluLo + (uint32_t)i - neg * kSiluSpan);
+      silu_tab[i] = silu_bf16(bf16_from_bits((uint16_t)bits));
+    }
+    __syncthreads();
+  }
   const int64_t cg = g.conv_dim / 8;
   const int64_t runs = (g.t + kConvRun - 1) / kConvRun;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t idx = (int64_t)blockIdx.x * kConvThreads + threadIdx.x;
   if (idx >= (int64_t)g.batch * runs * cg) return;
   const int c0 = (int)(idx % cg) * 8;
   const int64_t rr = idx / cg;
   const int t0 = (int)(rr % runs) * kConvRun, r = (int)(rr / runs);
-  switch (g.kernel) {
-    case 2: conv_run<T, 2>(g, r, t0, c0); break;
-    case 3: conv_run<T, 3>(g, r, t0, c0); break;
-    case 4: conv_run<T, 4>(g, r, t0, c0); break;
-    case 5: conv_run<T, 5>(g, r, t0, c0); break;
-    case 6: conv_run<T, 6>(g, r, t0, c0); break;
-    case 7: conv_run<T, 7>(g, r, t0, c0); break;
-    default: conv_run<T, 8>(g, r, t0, c0); break;
-  }
+  conv_run<T, K>(g, silu_tab, r, t0, c0);
 }
 
-// New conv state: the last K-1 columns of [state || x] (qwen35.rs:429).
+template <typename T, int K>
+void launch_conv_k(const GdnArgs& g, int64_t items, hipStream_t s) {
+  constexpr int n = conv_threads(K);
+  hipLaunchKernelGGL((gdn_conv_kernel<T, K>), dim3((unsigned)((items + n - 1) / n)), dim3(n), 0, s, g);
+}
+
 template <typename T>
-__global__ __launch_bounds__(256) void gdn_conv_state_kernel(GdnArgs g) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)g.batch * g.conv_dim) return;
-  const int c = (int)(idx % g.conv_dim), r = (int)(idx / g.conv_dim);
-  const int K = g.kernel;
-  const T* x = (const T*)g.mixed + r * g.mixed_sb;
-  const T* tail = g.conv_in ? (const T*)g.conv_in + r * g.conv_in_sb : nullptr;
-  T* out = (T*)g.conv_out + ((int64_t)r * g.conv_dim + c) * (K - 1);
-  for (int i = 0; i < K - 1; ++i) {
-    const int f = g.t + i;  // index into [state || x]
-    T v;
-    if (f < K - 1)
-      v = tail ? tail[(int64_t)c * (K - 1) + f] : from_f<T>(0.0f);
-    else
-      v = x[(int64_t)(f - (K - 1)) * g.mixed_st + c];
-    out[i] = v;
+void launch_conv(const GdnArgs& g, int64_t items, hipStream_t s) {
+  switch (g.kernel) {
+    case 2: launch_conv_k<T, 2>(g, items, s); break;
+    case 3: launch_conv_k<T, 3>(g, items, s); break;
+    case 4: launch_conv_k<T, 4>(g, items, s); break;
+    case 5: launch_conv_k<T, 5>(g, items, s); break;
+    case 6: launch_conv_k<T, 6>(g, items, s); break;
+    case 7: launch_conv_k<T, 7>(g, items, s); break;
+    default: launch_conv_k<T, 8>(g, items, s); break;
   }
 }
 
@@ -728,10 +822,18 @@ constexpr int kScanThreads = 512;
 
 template <bool kPrefetch>
 __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
-  __shared__ float S[kD * 20];     // state slice (dk x 16), updated in place
-  __shared__ float Vn0[kC * 20];   // new_values - k_cumdecay . S, first half of dk
-  __shared__ float Vn1[kC * 20];   // k_cumdecay . S, second half of dk
-  __shared__ float Opart[kC * 20]; // (q e^cum) . S, second half of dk
+  // 16-column tiles.  The prefetching loop stores row r at row
+  // r ^ ((r >> 2) & 3) of a 16-float stride: the B-operand reads (rows
+  // 4i .. 4i+3 across a wave) and the accumulator writes (rows 4fq + e) then
+  // both touch 64 distinct banks.  The one-chunk kernel keeps a 20-float
+  // stride (2-way conflicts on the reads): the swizzle's extra address
+  // registers would not fit its 128.
+  constexpr int kRow = kPrefetch ? 16 : 20;
+  __shared__ float S[kD * kRow];     // state slice (dk x 16), updated in place
+  __shared__ float Vn0[kC * kRow];   // new_values - k_cumdecay . S, first half of dk
+  __shared__ float Vn1[kC * kRow];   // k_cumdecay . S, second half of dk
+  __shared__ float Opart[kC * kRow]; // (q e^cum) . S, second half of dk
+  auto sx = [](int row, int col) { return kPrefetch ? (row ^ ((row >> 2) & 3)) * 16 + col : row * 20 + col; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rt = wave & 3, kh = wave >> 2;
@@ -746,7 +848,7 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
 
   for (int p = tid; p < kD * kW; p += kScanThreads) {
     const int i = p / kW, j = p % kW;
-    S[i * 20 + j] = g.s_in ? g.s_in[r * g.s_in_sb + ((int64_t)h * kD + i) * kD + col0 + j] : 0.0f;
+    S[sx(i, j)] = g.s_in ? g.s_in[r * g.s_in_sb + ((int64_t)h * kD + i) * kD + col0 + j] : 0.0f;
   }
   __syncthreads();
   // A operands of one chunk for this wave; every field is written on every
@@ -773,7 +875,9 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     }
     o.in[0] = ld4(rec + in_off);
     o.in[1] = ld4(rec + in_off + 512);
-    o.nvv = ld4(rec + nv_off);
+    // kh = 1 waves do not use new_values; the prefetching loop loads it
+    // anyway (loads under a branch defeat the compiler's wait tracking there)
+    o.nvv = (kPrefetch || kh == 0) ? ld4(rec + nv_off) : f32x4{};
     o.decay = rec[kRecDecay];
   };
   // the output of the previous chunk (kh = 0 waves): its first half and intra
@@ -784,7 +888,7 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
       // the four Opart reads go out together, ahead of the stores' branches
       float o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = out_prev[e] + Opart[(16 * rt + 4 * fq + e) * 20 + fm];
+      for (int e = 0; e < 4; ++e) o[e] = out_prev[e] + Opart[sx(16 * rt + 4 * fq + e, fm)];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = c * kC + 16 * rt + 4 * fq + e;
@@ -806,7 +910,7 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     // operands are read before the first MFMA and reused by (q e^cum) . S
     float sb[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sb[i] = S[(4 * (16 * kh + i) + fq) * 20 + fm];
+    for (int i = 0; i < 16; ++i) sb[i] = S[sx(4 * (16 * kh + i) + fq, fm)];
     __builtin_amdgcn_sched_barrier(0);
     f32x4v acc = {0, 0, 0, 0};
 #pragma unroll
@@ -827,15 +931,15 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     for (int e = 0; e < 4; ++e) {
       const int row = 16 * rt + 4 * fq + e;
       if (kh == 0)
-        Vn0[row * 20 + fm] = cur.nvv[e] - acc[e];
+        Vn0[sx(row, fm)] = cur.nvv[e] - acc[e];
       else
-        Vn1[row * 20 + fm] = acc[e];
+        Vn1[sx(row, fm)] = acc[e];
     }
     __syncthreads();
     // phase B
     float vb[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) vb[i] = Vn0[(4 * i + fq) * 20 + fm] - Vn1[(4 * i + fq) * 20 + fm];
+    for (int i = 0; i < 16; ++i) vb[i] = Vn0[sx(4 * i + fq, fm)] - Vn1[sx(4 * i + fq, fm)];
     __builtin_amdgcn_sched_barrier(0);
     f32x4v su = {0, 0, 0, 0}, ob = {0, 0, 0, 0};
 #pragma unroll
@@ -875,12 +979,12 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
       out_prev = ob;
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Opart[(16 * rt + 4 * fq + e) * 20 + fm] = ob[e];
+      for (int e = 0; e < 4; ++e) Opart[sx(16 * rt + 4 * fq + e, fm)] = ob[e];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int r0 = 16 * wave + 4 * fq + e;
-      S[r0 * 20 + fm] = S[r0 * 20 + fm] * cur.decay + su[e];
+      S[sx(r0, fm)] = S[sx(r0, fm)] * cur.decay + su[e];
     }
     __syncthreads();
   };
@@ -907,7 +1011,7 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
   store_out(g.n_chunks - 1);
   for (int p = tid; p < kD * kW; p += kScanThreads) {
     const int i = p / kW, j = p % kW;
-    g.s_out[((int64_t)r * g.nv + h) * kD * kD + (int64_t)i * kD + col0 + j] = S[i * 20 + j];
+    g.s_out[((int64_t)r * g.nv + h) * kD * kD + (int64_t)i * kD + col0 + j] = S[sx(i, j)];
   }
 }
 
@@ -1113,18 +1217,15 @@ extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, con
   g.eps = d->eps;
   hipStream_t s = (hipStream_t)stream;
   const int64_t conv_items = (int64_t)g.batch * ((g.t + kConvRun - 1) / kConvRun) * (g.conv_dim / 8);
-  const int64_t state_items = (int64_t)g.batch * g.conv_dim;
   const int64_t recs = (int64_t)g.batch * g.nv * g.n_chunks;
   const int64_t slices = ((int64_t)g.batch * g.nv + kXcds - 1) / kXcds * kXcds * (kD / kW);
   const int64_t norm_items = (int64_t)g.batch * g.t * g.nv;
-  if (recs > INT32_MAX || (conv_items + 255) / 256 > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "GDN grid too large");
+  if (recs > INT32_MAX || (conv_items + 511) / 512 > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "GDN grid too large");
   if (d->dtype == CEV_BF16) {
-    hipLaunchKernelGGL(gdn_conv_kernel<__bf16>, dim3((unsigned)((conv_items + 255) / 256)), dim3(256), 0, s, g);
-    hipLaunchKernelGGL(gdn_conv_state_kernel<__bf16>, dim3((unsigned)((state_items + 255) / 256)), dim3(256), 0, s, g);
+    launch_conv<__bf16>(g, conv_items, s);
     hipLaunchKernelGGL(gdn_prep_kernel<__bf16>, dim3((unsigned)recs), dim3(kPrepThreads), 0, s, g);
   } else {
-    hipLaunchKernelGGL(gdn_conv_kernel<float>, dim3((unsigned)((conv_items + 255) / 256)), dim3(256), 0, s, g);
-    hipLaunchKernelGGL(gdn_conv_state_kernel<float>, dim3((unsigned)((state_items + 255) / 256)), dim3(256), 0, s, g);
+    launch_conv<float>(g, conv_items, s);
     hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3((unsigned)recs), dim3(kPrepThreads), 0, s, g);
   }
   if (g.n_chunks > 1)

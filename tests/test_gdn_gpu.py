@@ -65,6 +65,29 @@ def test_gdn_small_vs_oracle(gpu, orc, bf16, t):
     assert ey <= (BF16_TOL if bf16 else F32_TOL)
 
 
+def test_gdn_conv_silu_outside_table(gpu, orc):
+    """bf16 conv outputs outside the SiLU table (|v| >= 128 and |v| < 2^-16):
+    q/k channels scaled by 400 and by 1e-6, so every token of the q/k waves
+    takes the per-element SiLU while the v waves use the table.  l2norm
+    removes the scale, so the bars are those of the other cases."""
+    w = configs.GdnWorkload("gdn-silu-range", 12, True, 1, 150, nk=2, nv=4)
+    _say(f"test gdn silu range: B={w.batch} T={w.t}")
+    inp = w.inputs()
+    qk = 2 * w.nk * w.dk
+    m = inp["mixed"].copy()
+    m[..., : qk // 3] *= 400.0
+    m[..., qk // 3: 2 * qk // 3] *= 1e-6
+    inp["mixed"] = cev_hip.synth.round_bf16(m)
+    y, co, so = _run_gpu(w, inp, gpu)
+    ry, rco, rso = _run_oracle(orc, w, inp)
+    ey = float(np.abs(to_np(y) - ry).max())
+    es = float(np.abs(to_np(so) - rso).max())
+    _say(f"  max|dy| {ey:.3g} max|dS| {es:.3g}")
+    assert np.array_equal(to_np(co), rco)
+    assert es <= F32_TOL
+    assert ey <= BF16_TOL
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_gdn_carried_state_vs_oracle(gpu, orc, bf16):
     """conv_in / s_in given (a prefix already consumed), one state broadcast
