@@ -90,19 +90,22 @@ struct GdnArgs {
   float* rec;    // workspace: (B, nv, n_chunks) records
   float* core;   // workspace: (B, T, nv, dv) f32
   int64_t mixed_sb, mixed_st, z_sb, z_st, ab_sb, ab_st, conv_in_sb, s_in_sb, y_sb, y_st;
-  int32_t batch, t, nk, nv, kernel, conv_dim, n_chunks;
+  int32_t batch, t, nk, nv, kernel, conv_dim, n_chunks, conv_run;
   float eps;
 };
 
 // ---------------------------------------------------------------------------
-// conv + SiLU.  Thread = (row, 8 channels, run of kConvRun tokens): the 8 x K
+// conv + SiLU.  Thread = (row, 8 channels, run of conv_run tokens): the 8 x K
 // weights stay in registers and the last K-1 input rows slide through a
 // register window, so every input row is read once as one 16-byte vector.
 // Each product and partial sum is one model-dtype op (decoder.rs:143-150);
 // SiLU is candle's v / (1 + exp(-v)) with each op in the model dtype.  The
 // thread of a row's last run also writes the new conv state: its window then
 // holds the last K-1 columns of [state || x] (qwen35.rs:429).
-constexpr int kConvRun = 16;
+// Run length: 16 tokens, or 8 / 4 when that leaves fewer workgroups than
+// CUs (short rows, e.g. 32 rows of 64 tokens).
+constexpr int kConvRunMax = 16;
+constexpr int kConvCus = 256;
 // 16 waves per workgroup share one table; widths 7 and 8 need more than the
 // 128 registers that leaves each lane, so they run 8 waves
 constexpr int conv_threads(int K) { return K <= 6 ? 1024 : 512; }
@@ -211,7 +214,7 @@ __device__ __forceinline__ void conv_run(const GdnArgs& g, const float* silu_tab
     }
   }
   T* out = (T*)g.conved + ((int64_t)r * g.t + t0) * g.conv_dim + c0;
-  const int n = min(kConvRun, g.t - t0);
+  const int n = min(g.conv_run, g.t - t0);
   // the next row loads while this one is computed (the last load repeats
   // the last row, so it stays unconditional and in bounds)
   Raw8<T> next;
@@ -291,12 +294,12 @@ __global__ __launch_bounds__(conv_threads(K)) void gdn_conv_kernel(GdnArgs g) {
     __syncthreads();
   }
   const int64_t cg = g.conv_dim / 8;
-  const int64_t runs = (g.t + kConvRun - 1) / kConvRun;
+  const int64_t runs = (g.t + g.conv_run - 1) / g.conv_run;
   const int64_t idx = (int64_t)blockIdx.x * kConvThreads + threadIdx.x;
   if (idx >= (int64_t)g.batch * runs * cg) return;
   const int c0 = (int)(idx % cg) * 8;
   const int64_t rr = idx / cg;
-  const int t0 = (int)(rr % runs) * kConvRun, r = (int)(rr / runs);
+  const int t0 = (int)(rr % runs) * g.conv_run, r = (int)(rr / runs);
   conv_run<T, K>(g, silu_tab, r, t0, c0);
 }
 
@@ -1216,7 +1219,11 @@ extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, con
   g.n_chunks = (d->t + kC - 1) / kC;
   g.eps = d->eps;
   hipStream_t s = (hipStream_t)stream;
-  const int64_t conv_items = (int64_t)g.batch * ((g.t + kConvRun - 1) / kConvRun) * (g.conv_dim / 8);
+  const int conv_wg = conv_threads(g.kernel);
+  auto conv_items_of = [&](int run) { return (int64_t)g.batch * ((g.t + run - 1) / run) * (g.conv_dim / 8); };
+  g.conv_run = kConvRunMax;
+  while (g.conv_run > 4 && conv_items_of(g.conv_run) < (int64_t)kConvCus * conv_wg) g.conv_run /= 2;
+  const int64_t conv_items = conv_items_of(g.conv_run);
   const int64_t recs = (int64_t)g.batch * g.nv * g.n_chunks;
   const int64_t slices = ((int64_t)g.batch * g.nv + kXcds - 1) / kXcds * kXcds * (kD / kW);
   const int64_t norm_items = (int64_t)g.batch * g.t * g.nv;
