@@ -41,13 +41,31 @@ constexpr int kSC = 68;    // LDS row stride of 64-wide f32 tiles
 //   In  intra             A operand, row tile w:   [w 4][j 4][lane][4] = In[16w + l%16][4(4j+e) + l/16]
 //   Nv  new_values        accumulator, slice sl:   [sl 8][w 4][lane][4] = Nv[16w + 4(l/16) + e][16sl + l%16]
 //   decay                 e^last
-constexpr int kRecQd = 0;
-constexpr int kRecKc = kRecQd + kC * kD;
-constexpr int kRecKd = kRecKc + kC * kD;
-constexpr int kRecNv = kRecKd + kC * kD;
-constexpr int kRecIn = kRecNv + kC * kD;
-constexpr int kRecDecay = kRecIn + kC * kC;
-constexpr int kRecFloats = kRecDecay + 16;
+// bf16 models keep q and k as the raw bf16 conv output instead of Qd and Kd,
+// 16 values per lane in 32 bytes, plus the factors prep multiplies them by:
+//   Qb  [w 4][K half 2][lane][j' 4][e 4] = q[16w + l%16][4(4(4 half + j') + e) + l/16]
+//   Kb  [ti 8][lane][j 4][e 4]            = k[4(4j+e) + l/16][16ti + l%16]
+//   Qf  [row][2] = (dk^-0.5 / |q_row|, e^cum_row)
+//   Kf  [2][l/16][m 16] = 1 / |k_t| and e^(last - cum_t) of token t = 4m + l/16
+// The scan rebuilds Qd = (q * Qf0) * Qf1 and Kd = (k * 1/|k|) * e^(last - cum)
+// with prep's own two roundings, so both layouts give the same bits; the bf16
+// record is 113 KB instead of 144 KB.
+template <bool BF>
+struct RecLayout;
+template <>
+struct RecLayout<false> {
+  static constexpr int Qd = 0, Kc = kC * kD, Kd = 2 * kC * kD, Nv = 3 * kC * kD, In = 4 * kC * kD;
+  static constexpr int Decay = In + kC * kC, Qf = Decay, Kf = Decay;  // no factors
+  static constexpr int Floats = Decay + 16;
+};
+template <>
+struct RecLayout<true> {
+  static constexpr int Qd = 0, Kc = kC * kD / 2, Kd = Kc + kC * kD, Nv = Kd + kC * kD / 2, In = Nv + kC * kD;
+  static constexpr int Decay = In + kC * kC, Qf = Decay + 16, Kf = Qf + 2 * kC;
+  static constexpr int Floats = Kf + 2 * kC;
+};
+constexpr int kRecFloats = RecLayout<false>::Floats;  // the workspace's record size (the larger one)
+static_assert(RecLayout<true>::Floats % 16 == 0 && RecLayout<false>::Floats % 16 == 0, "64-byte aligned records");
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
@@ -391,7 +409,7 @@ static_assert(kC * kSX * sizeof(float) <= 2 * kC * kSB * sizeof(__bf16), "k_cumd
 //   intra[i][j] = QK[i][j] pair[i][j] for j <= i  (qwen35.rs:318-330),
 // ut into Us; intra through the wave's own tile of Tm into its record order.
 template <bool DG, bool DQ, typename LT>
-__device__ __forceinline__ void prep_tile_store(LT& L, float* rec, int ti, int tj, int lane, const f32x4v& gacc, const f32x4v& qacc) {
+__device__ __forceinline__ void prep_tile_store(LT& L, float* rec_in, int ti, int tj, int lane, const f32x4v& gacc, const f32x4v& qacc) {
   const int fm = lane & 15, fq = lane >> 4;
   const int j = 16 * tj + fm;
 #pragma unroll
@@ -406,7 +424,7 @@ __device__ __forceinline__ void prep_tile_store(LT& L, float* rec, int ti, int t
     f32x4 v;
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = L.Tm[(16 * ti + fm) * kSC + 16 * tj + 4 * e + fq];
-    *(f32x4*)(rec + kRecIn + 4 * ((ti * 4 + tj) * 64 + lane)) = v;
+    *(f32x4*)(rec_in + 4 * ((ti * 4 + tj) * 64 + lane)) = v;
   }
 }
 
@@ -418,7 +436,7 @@ __device__ __forceinline__ void prep_tile_store(LT& L, float* rec, int ti, int t
 // Lane (fm, fq) reads row 16 t + fm, columns 32 s + 8 fq .. + 7 (16 bytes)
 // of A and B, so both operands pair up over the same k.
 template <bool DG, bool DQ>
-__device__ __forceinline__ void prep_tile_bf16(PrepLds<true>& L, float* rec, int ti, int tj, int lane) {
+__device__ __forceinline__ void prep_tile_bf16(PrepLds<true>& L, float* rec_in, int ti, int tj, int lane) {
   const int fm = lane & 15, fq = lane >> 4;
   const __bf16* ka = L.Kb + (16 * ti + fm) * kSB + 8 * fq;
   const __bf16* qa = L.Qb + (16 * ti + fm) * kSB + 8 * fq;
@@ -437,14 +455,14 @@ __device__ __forceinline__ void prep_tile_bf16(PrepLds<true>& L, float* rec, int
     if (DG) gacc[e] = gacc[e] * (L.betas[i] * L.kf[i]) * kfj;
     if (DQ) qacc[e] = qacc[e] * L.qf[i] * kfj;
   }
-  prep_tile_store<DG, DQ>(L, rec, ti, tj, lane, gacc, qacc);
+  prep_tile_store<DG, DQ>(L, rec_in, ti, tj, lane, gacc, qacc);
 }
 
 // One 16x16 tile (ti, tj), tj <= ti, of G = (k beta) k^T (DG) and / or
 // QK = q k^T (DQ) on the normalised f32 rows.  The k-sum runs in the order
 // 16j + 4fq + e, so each lane reads its A and B operands as 16-byte vectors.
 template <bool DG, bool DQ, typename LT>
-__device__ __forceinline__ void prep_tile(LT& L, float* rec, int ti, int tj, int lane) {
+__device__ __forceinline__ void prep_tile(LT& L, float* rec_in, int ti, int tj, int lane) {
   const int fm = lane & 15, fq = lane >> 4;
   const float* ka = L.Ks + (16 * ti + fm) * kSX + 4 * fq;
   const float* qa = L.Qs + (16 * ti + fm) * kSX + 4 * fq;
@@ -463,7 +481,7 @@ __device__ __forceinline__ void prep_tile(LT& L, float* rec, int ti, int tj, int
       if (DQ) qacc = mma16(q4[e], b4[e], qacc);
     }
   }
-  prep_tile_store<DG, DQ>(L, rec, ti, tj, lane, gacc, qacc);
+  prep_tile_store<DG, DQ>(L, rec_in, ti, tj, lane, gacc, qacc);
 }
 
 // 16x16 diagonal block b of inv = (I + L)^-1, L = Us strict lower, by
@@ -502,6 +520,7 @@ __device__ __forceinline__ void prep_inv16(LT& L, int b, int lane) {
 template <typename T>
 __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   constexpr bool BF = std::is_same<T, __bf16>::value;
+  using R = RecLayout<BF>;
   __shared__ PrepLds<BF> L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fm = lane & 15, fq = lane >> 4;  // fragment row / k-slot of this lane
@@ -512,7 +531,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   const int key_dim = g.nk * kD;
   const int t0 = c * kC;
   const T* cv = (const T*)g.conved + (int64_t)r * g.t * g.conv_dim;
-  float* rec = g.rec + (int64_t)blockIdx.x * kRecFloats;
+  float* rec = g.rec + (int64_t)blockIdx.x * R::Floats;
 
   // All loads below read a valid row (clamped to the last token) and the
   // rows past t are zeroed afterwards, so no load sits behind a branch and
@@ -611,7 +630,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
     L.cums[lane] = acc;
     L.ecum[lane] = expf(acc);
     L.ekd[lane] = expf(last - acc);
-    if (lane == 0) rec[kRecDecay] = expf(last);
+    if (lane == 0) rec[R::Decay] = expf(last);
   }
   __syncthreads();
 
@@ -632,9 +651,9 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   auto tile = [&](auto dg_c, auto dq_c, int ti, int tj) {
     constexpr bool DG = decltype(dg_c)::value, DQ = decltype(dq_c)::value;
     if constexpr (BF)
-      prep_tile_bf16<DG, DQ>(L, rec, ti, tj, lane);
+      prep_tile_bf16<DG, DQ>(L, rec + R::In, ti, tj, lane);
     else
-      prep_tile<DG, DQ>(L, rec, ti, tj, lane);
+      prep_tile<DG, DQ>(L, rec + R::In, ti, tj, lane);
   };
   using Yes = std::true_type;
   using No = std::false_type;
@@ -668,36 +687,70 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
       return L.Ks[i * kSX + c];
   };
   // Records the inversion's idle waves write: q e^cum (Qd) and k e^(last -
-  // cum) (Kd) in their fragment orders, and intra's six zero tiles.
+  // cum) (Kd) in their fragment orders (bf16 models: the raw rows and their
+  // factors), and intra's six zero tiles.
+  constexpr int kQdStores = BF ? kC * kD / 8 : kC * kD / 4;  // 16-byte stores per record part
   auto qd_records = [&](int p0, int step) {
-    for (int p = p0; p < kC * kD / 4; p += step) {
-      const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;  // [w 4][j 8][lane]
-      f32x4 v;
+    for (int p = p0; p < kQdStores; p += step) {
+      if constexpr (BF) {
+        const int hf = p & 1, l = (p >> 1) & 63, half = (p >> 7) & 1, w = p >> 8;  // [w 4][half 2][lane][hf 2]
+        bf16x8 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 16 * w + (l & 15), k = 4 * (4 * j + e) + (l >> 4);
-        v[e] = q_hat(i, k) * L.ecum[i];
+        for (int x = 0; x < 8; ++x) {
+          const int j = 4 * half + 2 * hf + (x >> 2), e = x & 3;
+          v[x] = L.Qb[(16 * w + (l & 15)) * kSB + 4 * (4 * j + e) + (l >> 4)];
+        }
+        *(bf16x8*)(rec + R::Qd + 4 * p) = v;
+      } else {
+        const int l = p & 63, j = (p >> 6) & 7, w = p >> 9;  // [w 4][j 8][lane]
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * w + (l & 15), k = 4 * (4 * j + e) + (l >> 4);
+          v[e] = q_hat(i, k) * L.ecum[i];
+        }
+        *(f32x4*)(rec + R::Qd + 4 * p) = v;
       }
-      *(f32x4*)(rec + kRecQd + 4 * p) = v;
     }
   };
   auto kd_records = [&](int p0, int p_end, int step) {
     for (int p = p0; p < p_end; p += step) {
-      const int l = p & 63, jj = (p >> 6) & 3, ti = p >> 8;  // [ti 8][j 4][lane]
-      f32x4 u;
+      if constexpr (BF) {
+        const int hf = p & 1, l = (p >> 1) & 63, ti = p >> 7;  // [ti 8][lane][hf 2]
+        bf16x8 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 4 * (4 * jj + e) + (l >> 4), col = 16 * ti + (l & 15);
-        u[e] = k_hat(i, col) * L.ekd[i];
+        for (int x = 0; x < 8; ++x) {
+          const int j = 2 * hf + (x >> 2), e = x & 3;
+          v[x] = L.Kb[(4 * (4 * j + e) + (l >> 4)) * kSB + 16 * ti + (l & 15)];
+        }
+        *(bf16x8*)(rec + R::Kd + 4 * p) = v;
+      } else {
+        const int l = p & 63, jj = (p >> 6) & 3, ti = p >> 8;  // [ti 8][j 4][lane]
+        f32x4 u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * (4 * jj + e) + (l >> 4), col = 16 * ti + (l & 15);
+          u[e] = k_hat(i, col) * L.ekd[i];
+        }
+        *(f32x4*)(rec + R::Kd + 4 * p) = u;
       }
-      *(f32x4*)(rec + kRecKd + 4 * p) = u;
+    }
+  };
+  // bf16 models: the row factors of q and the token factors of k
+  auto factor_records = [&](int i) {
+    if constexpr (BF) {
+      if (i < kC) {
+        *(f32x2v*)(rec + R::Qf + 2 * i) = f32x2v{L.qf[i], L.ecum[i]};
+        rec[R::Kf + (i & 3) * 16 + (i >> 2)] = L.kf[i];
+        rec[R::Kf + kC + (i & 3) * 16 + (i >> 2)] = L.ekd[i];
+      }
     }
   };
   auto zero_intra = [&](int p0, int step) {
     for (int p = p0; p < 6 * 64; p += step) {
       const int q = p >> 6;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
       const int ti = q < 3 ? 0 : (q < 5 ? 1 : 2), tj = q < 3 ? q + 1 : (q < 5 ? q - 1 : 3);
-      *(f32x4*)(rec + kRecIn + 4 * ((ti * 4 + tj) * 64 + (p & 63))) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      *(f32x4*)(rec + R::In + 4 * ((ti * 4 + tj) * 64 + (p & 63))) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
   };
 
@@ -750,8 +803,9 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.Tm[(16 * ti2 + 4 * fq + e) * kSC + 16 * tj2 + fm] = bc[e];
   } else {
-    kd_records(tid - 256, kC * kD / 8, 256);
+    kd_records(tid - 256, kQdStores / 2, 256);
     zero_intra(tid - 256, 256);
+    factor_records(tid - 256);
   }
   __syncthreads();
   if (wave < 4) {
@@ -761,7 +815,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.iv(32 + 16 * ti2 + 4 * fq + e, 16 * tj2 + fm) = -x[e];
   } else {
-    kd_records(kC * kD / 8 + tid - 256, kC * kD / 4, 256);
+    kd_records(kQdStores / 2 + tid - 256, kQdStores, 256);
   }
   __syncthreads();
 
@@ -786,7 +840,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
         kc = mma16(a4[jg][e], kreg[4 * jg + e], kc);
       }
     }
-    *(f32x4*)(rec + kRecNv + ((wave * 4 + ti) * 64 + lane) * 4) = f32x4{nv[0], nv[1], nv[2], nv[3]};
+    *(f32x4*)(rec + R::Nv + ((wave * 4 + ti) * 64 + lane) * 4) = f32x4{nv[0], nv[1], nv[2], nv[3]};
 #pragma unroll
     for (int e = 0; e < 4; ++e) stage[(16 * ti + 4 * fq + e) * kSX + 16 * wave + fm] = kc[e];
   }
@@ -796,7 +850,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
     f32x4 v;
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = stage[(16 * ti + fm) * kSX + 16 * wave + 4 * e + fq];
-    *(f32x4*)(rec + kRecKc + 4 * ((ti * 8 + wave) * 64 + lane)) = v;
+    *(f32x4*)(rec + R::Kc + 4 * ((ti * 8 + wave) * 64 + lane)) = v;
   }
 }
 
@@ -823,8 +877,28 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 constexpr int kXcds = 8;
 constexpr int kScanThreads = 512;
 
-template <bool kPrefetch>
+// A operands of one chunk for one wave; every field is written on every path
+// (a struct written on one branch only is kept in scratch memory).  bf16
+// records hold raw q / k rows and their factors instead of Qd / Kd.
+template <bool BF>
+struct ScanOps;
+template <>
+struct ScanOps<false> {
+  f32x4 kc[4], qd[4], kd[4], in[2], nvv;
+  float decay;
+};
+template <>
+struct ScanOps<true> {
+  f32x4 kc[4], in[2], nvv;
+  bf16x8 qb[2], kb[2];
+  f32x2v qf, kf;  // this lane's (dk^-0.5/|q|, e^cum) row factors; its part of the Kf array
+  float decay;
+};
+
+template <bool kPrefetch, bool BF>
 __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
+  using R = RecLayout<BF>;
+  using Ops = ScanOps<BF>;
   // 16-column tiles.  The prefetching loop stores row r at row
   // r ^ ((r >> 2) & 3) of a 16-float stride: the B-operand reads (rows
   // 4i .. 4i+3 across a wave) and the accumulator writes (rows 4fq + e) then
@@ -836,6 +910,7 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
   __shared__ float Vn0[kC * kRow];   // new_values - k_cumdecay . S, first half of dk
   __shared__ float Vn1[kC * kRow];   // k_cumdecay . S, second half of dk
   __shared__ float Opart[kC * kRow]; // (q e^cum) . S, second half of dk
+  __shared__ float KF[BF ? 2 * kC : 1];  // bf16: the chunk's Kf array
   auto sx = [](int row, int col) { return kPrefetch ? (row ^ ((row >> 2) & 3)) * 16 + col : row * 20 + col; };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -849,39 +924,51 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
   const int col0 = sl * kW;
   const int fm = lane & 15, fq = lane >> 4;
 
-  for (int p = tid; p < kD * kW; p += kScanThreads) {
-    const int i = p / kW, j = p % kW;
-    S[sx(i, j)] = g.s_in ? g.s_in[r * g.s_in_sb + ((int64_t)h * kD + i) * kD + col0 + j] : 0.0f;
-  }
-  __syncthreads();
-  // A operands of one chunk for this wave; every field is written on every
-  // path (a struct written on one branch only is kept in scratch memory).
-  struct Ops {
-    f32x4 kc[4], qd[4], kd[4], in[2], nvv;
-    float decay;
-  };
   // this lane's float offsets inside a record: kc / qd operand j at + 256 j,
-  // kd operand j at + 256 j, intra blocks kh and kh + 2 at + 0 and + 512
-  const int kc_off = kRecKc + 4 * (rt * 8 * 64 + 4 * kh * 64 + lane);
-  const int qd_off = kRecQd + 4 * (rt * 8 * 64 + 4 * kh * 64 + lane);
-  const int kd_off = kRecKd + 4 * (wave * 4 * 64 + lane);
-  const int in_off = kRecIn + 4 * (rt * 4 * 64 + kh * 64 + lane);
-  const int nv_off = kRecNv + 4 * ((sl * 4 + rt) * 64 + lane);  // read by kh = 0 only
-  auto rec_at = [&](int c) { return g.rec + ((int64_t)item * g.n_chunks + c) * kRecFloats; };
+  // kd operand j at + 256 j, intra blocks kh and kh + 2 at + 0 and + 512;
+  // bf16 q and k rows at + 0 and + 4 (two 16-byte halves)
+  const int kc_off = R::Kc + 4 * (rt * 8 * 64 + 4 * kh * 64 + lane);
+  const int qd_off = BF ? R::Qd + 8 * ((rt * 2 + kh) * 64 + lane) : R::Qd + 4 * (rt * 8 * 64 + 4 * kh * 64 + lane);
+  const int kd_off = BF ? R::Kd + 8 * (wave * 64 + lane) : R::Kd + 4 * (wave * 4 * 64 + lane);
+  const int in_off = R::In + 4 * (rt * 4 * 64 + kh * 64 + lane);
+  const int nv_off = R::Nv + 4 * ((sl * 4 + rt) * 64 + lane);  // read by kh = 0 only
+  const int qf_off = R::Qf + 2 * (16 * rt + fm);
+  const int kf_off = R::Kf + 2 * lane;
+  auto rec_at = [&](int c) { return g.rec + ((int64_t)item * g.n_chunks + c) * R::Floats; };
   auto ld4 = [](const float* p) { return *(const f32x4*)p; };
-  auto fetch = [&](const float* rec, Ops& o) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o.kc[j] = ld4(rec + kc_off + 256 * j);
+  auto ldb = [](const float* p) { return *(const bf16x8*)p; };
+  auto ld2 = [](const float* p) { return *(const f32x2v*)p; };
+  // the phase-A operands (k_cumdecay, new_values, decay; the Kf array), the
+  // phase-B ones (q e^cum or q, k e^(last - cum) or k, intra; the q factors)
+  auto fetch_a = [&](const float* rec, Ops& o, int j) {
+    o.kc[j] = ld4(rec + kc_off + 256 * j);
+    if (j == 3) {
+      // kh = 1 waves do not use new_values; the prefetching loop loads it
+      // anyway (loads under a branch defeat the compiler's wait tracking there)
+      o.nvv = (kPrefetch || kh == 0) ? ld4(rec + nv_off) : f32x4{};
+      o.decay = rec[R::Decay];
+      if constexpr (BF) o.kf = ld2(rec + kf_off);
+    }
+  };
+  auto fetch_b = [&](const float* rec, Ops& o, int j) {
+    if constexpr (BF) {
+      if (j < 2) {
+        o.qb[j] = ldb(rec + qd_off + 4 * j);
+        o.kb[j] = ldb(rec + kd_off + 4 * j);
+      }
+      if (j == 2) o.qf = ld2(rec + qf_off);
+    } else {
       o.qd[j] = ld4(rec + qd_off + 256 * j);
       o.kd[j] = ld4(rec + kd_off + 256 * j);
     }
-    o.in[0] = ld4(rec + in_off);
-    o.in[1] = ld4(rec + in_off + 512);
-    // kh = 1 waves do not use new_values; the prefetching loop loads it
-    // anyway (loads under a branch defeat the compiler's wait tracking there)
-    o.nvv = (kPrefetch || kh == 0) ? ld4(rec + nv_off) : f32x4{};
-    o.decay = rec[kRecDecay];
+    if (j < 2) o.in[j] = ld4(rec + in_off + 512 * j);
+  };
+  auto fetch = [&](const float* rec, Ops& o) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      fetch_a(rec, o, j);
+      fetch_b(rec, o, j);
+    }
   };
   // the output of the previous chunk (kh = 0 waves): its first half and intra
   // term in registers, the second half in Opart
@@ -914,19 +1001,39 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     float sb[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) sb[i] = S[sx(4 * (16 * kh + i) + fq, fm)];
+    // bf16: q e^cum and k e^(last - cum) are rebuilt here, one k-step group
+    // per MFMA group, so the VALU work runs beside the chain and phase B's
+    // MFMAs read finished operands; the k factors of this lane's tokens
+    // 4m + fq come from the chunk's Kf array in LDS
+    // (read ahead of the MFMAs in the prefetching loop; the one-chunk
+    // kernel, held to 128 registers, reads each group's just before use)
+    f32x4 kf4[BF ? 4 : 1], ek4[BF ? 4 : 1];
+    float qdf[BF ? 16 : 1], kdf[BF ? 16 : 1];
+    auto k_factors = [&](int j) {
+      kf4[j] = *(const f32x4*)(KF + 16 * fq + 4 * j);
+      ek4[j] = *(const f32x4*)(KF + kC + 16 * fq + 4 * j);
+    };
+    if constexpr (BF && kPrefetch) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) k_factors(j);
+    }
     __builtin_amdgcn_sched_barrier(0);
     f32x4v acc = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc = mma16(cur.kc[j][e], sb[4 * j + e], acc);
+      if constexpr (BF) {
+        if constexpr (!kPrefetch) k_factors(j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qdf[4 * j + e] = ((float)cur.qb[j >> 1][(j & 1) * 4 + e] * cur.qf[0]) * cur.qf[1];
+          kdf[4 * j + e] = ((float)cur.kb[j >> 1][(j & 1) * 4 + e] * kf4[j][e]) * ek4[j][e];
+        }
+      }
       if (kPrefetch) {
         __builtin_amdgcn_sched_barrier(0);
-        nxt.kc[j] = ld4(nrec + kc_off + 256 * j);
-        if (j == 3) {
-          nxt.nvv = ld4(nrec + nv_off);
-          nxt.decay = nrec[kRecDecay];
-        }
+        fetch_a(nrec, nxt, j);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -949,14 +1056,20 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        su = mma16(cur.kd[j][e], vb[4 * j + e], su);
-        ob = mma16(cur.qd[j][e], sb[4 * j + e], ob);
+        float kd, qd;
+        if constexpr (BF) {
+          kd = kdf[4 * j + e];
+          qd = qdf[4 * j + e];
+        } else {
+          kd = cur.kd[j][e];
+          qd = cur.qd[j][e];
+        }
+        su = mma16(kd, vb[4 * j + e], su);
+        ob = mma16(qd, sb[4 * j + e], ob);
       }
       if (kPrefetch) {
         __builtin_amdgcn_sched_barrier(0);
-        nxt.qd[j] = ld4(nrec + qd_off + 256 * j);
-        nxt.kd[j] = ld4(nrec + kd_off + 256 * j);
-        if (j < 2) nxt.in[j] = ld4(nrec + in_off + 512 * j);
+        fetch_b(nrec, nxt, j);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -989,10 +1102,20 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
       const int r0 = 16 * wave + 4 * fq + e;
       S[sx(r0, fm)] = S[sx(r0, fm)] * cur.decay + su[e];
     }
+    // the next chunk's Kf array, read in its phase A; every wave writes the
+    // same values (keeps the load unconditional).  Only the prefetching loop
+    // has a next chunk: the one-chunk kernel runs a single chunk.
+    if constexpr (BF && kPrefetch) *(f32x2v*)(KF + 2 * lane) = nxt.kf;
     __syncthreads();
   };
   Ops ops_a, ops_b;
   fetch(rec_at(0), ops_a);
+  for (int p = tid; p < kD * kW; p += kScanThreads) {
+    const int i = p / kW, j = p % kW;
+    S[sx(i, j)] = g.s_in ? g.s_in[r * g.s_in_sb + ((int64_t)h * kD + i) * kD + col0 + j] : 0.0f;
+  }
+  if constexpr (BF) *(f32x2v*)(KF + 2 * lane) = ops_a.kf;  // chunk 0's
+  __syncthreads();
   if constexpr (kPrefetch) {
     // Two chunks per iteration so the operand sets alternate without a copy
     // (a copy would wait for every prefetch to land).  The prefetch address
@@ -1019,12 +1142,16 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
 }
 
 // Many chunks: the prefetching loop (up to 256 VGPRs, one workgroup per CU).
-__global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) { gdn_scan<true>(g); }
+template <bool BF>
+__global__ __launch_bounds__(kScanThreads) void gdn_scan_kernel(GdnArgs g) {
+  gdn_scan<true, BF>(g);
+}
 // One chunk per (row, head): no loop to prefetch across, so the registers
 // are held to 128 and two workgroups share a CU, one loading while the
 // other computes.
+template <bool BF>
 __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(4))) void gdn_scan_one_chunk_kernel(GdnArgs g) {
-  gdn_scan<false>(g);
+  gdn_scan<false, BF>(g);
 }
 
 // ---------------------------------------------------------------------------
@@ -1235,10 +1362,18 @@ extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, con
     launch_conv<float>(g, conv_items, s);
     hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3((unsigned)recs), dim3(kPrepThreads), 0, s, g);
   }
-  if (g.n_chunks > 1)
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
-  else
-    hipLaunchKernelGGL(gdn_scan_one_chunk_kernel, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
+  const bool bf = d->dtype == CEV_BF16;
+  if (g.n_chunks > 1) {
+    if (bf)
+      hipLaunchKernelGGL(gdn_scan_kernel<true>, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
+    else
+      hipLaunchKernelGGL(gdn_scan_kernel<false>, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
+  } else {
+    if (bf)
+      hipLaunchKernelGGL(gdn_scan_one_chunk_kernel<true>, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
+    else
+      hipLaunchKernelGGL(gdn_scan_one_chunk_kernel<false>, dim3((unsigned)slices), dim3(kScanThreads), 0, s, g);
+  }
   // 16-byte aligned rows of z and y (and norm_w) for the vector norm
   const int64_t vec = d->dtype == CEV_BF16 ? 8 : 4;
   const bool norm_vec = ((uintptr_t)g.z | (uintptr_t)g.y | (uintptr_t)g.norm_w) % 16 == 0 && g.z_sb % vec == 0 && g.z_st % vec == 0 &&
