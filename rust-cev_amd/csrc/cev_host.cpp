@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <utility>
 #include <string>
 #include <vector>
 
@@ -279,9 +280,9 @@ int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, P
   std::vector<int32_t> order(n);
   for (int32_t i = 0; i < n; ++i) order[i] = i;
   std::sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return blocks[a].q_begin < blocks[b].q_begin; });
-  // Runs of adjacent blocks sharing their span list.
-  size_t oi = 0;
-  while (oi < order.size()) {
+  // Runs of adjacent blocks sharing their span list: [order[oi], order[oj]).
+  std::vector<std::pair<size_t, size_t>> runs;
+  for (size_t oi = 0; oi < order.size();) {
     size_t oj = oi + 1;
     while (oj < order.size()) {
       const cev_block& prev = blocks[order[oj - 1]];
@@ -289,11 +290,33 @@ int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, P
       if (cur.q_begin != prev.q_begin + prev.q_len || !same_spans(cur, blocks[order[oi]])) break;
       ++oj;
     }
-    const cev_block& first = blocks[order[oi]];
-    const cev_block& last = blocks[order[oj - 1]];
-    const int32_t r0 = first.q_begin, r1 = last.q_begin + last.q_len;
-    for (int32_t tr = r0; tr < r1; tr += p.tile_rows) {
-      const int32_t te = std::min(r1, tr + p.tile_rows);
+    runs.push_back({oi, oj});
+    oi = oj;
+  }
+  auto run_rows = [&](std::pair<size_t, size_t> u) {
+    const cev_block& first = blocks[order[u.first]];
+    const cev_block& last = blocks[order[u.second - 1]];
+    return std::make_pair(first.q_begin, last.q_begin + last.q_len);
+  };
+  // Rows per tile: a workgroup's tile_rows, or half of it for f32 plans whose
+  // full tiles would fill at most half of one round of kSplitTargetWorkgroups.
+  // An f32 key tile is MFMA-heavy, so a half-full workgroup takes about half
+  // the time per key tile, and twice the workgroups spread the work over more
+  // CUs (c1: K2 41.6 -> 32.4 us).  bf16 key tiles are fetch-bound: half-full
+  // tiles measured slower than splitting the key stream (c5a: 261 against
+  // 202 us), and on a full GPU half-full tiles would idle half the waves.
+  int64_t full_tiles = 0;
+  for (auto u : runs) {
+    const auto rr = run_rows(u);
+    full_tiles += (rr.second - rr.first + p.tile_rows - 1) / p.tile_rows;
+  }
+  const bool half = d->dtype == CEV_F32 && 2 * full_tiles * d->n_kv_heads <= kSplitTargetWorkgroups && p.tile_rows >= 2;
+  const int32_t step = half ? p.tile_rows / 2 : p.tile_rows;
+  for (auto u : runs) {
+    const cev_block& first = blocks[order[u.first]];
+    const int32_t r0 = run_rows(u).first, r1 = run_rows(u).second;
+    for (int32_t tr = r0; tr < r1; tr += step) {
+      const int32_t te = std::min(r1, tr + step);
       const int32_t seg_begin = p.n_segs;
       for (int s = 0; s < first.n_spans; ++s) push_seg(p, first.spans[s].begin, first.spans[s].begin + first.spans[s].len, 0, d->s_cache);
       // Local keys of the tile's rows: the part every row sees, and the union.
@@ -332,7 +355,6 @@ int32_t build_plan(const cev_attn_desc* d, const cev_block* blocks, int32_t n, P
       p.tiles.insert(p.tiles.end(), {tr, te - tr, seg_begin, p.n_segs - seg_begin, chunks, 0, 0, 0});
       p.n_tiles++;
     }
-    oi = oj;
   }
   // Split the key stream of every tile when that shortens the launch (few
   // long-prefix rows leave the GPU underfilled): each part still gets at

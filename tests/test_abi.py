@@ -389,11 +389,16 @@ def test_split_policy(cev):
     tab = cev_hip.BlockTable.from_rows(32, 64, 4096, causal=True)
     d = cev_hip.attn_desc(CEV_BF16, 16, 4, 256, tab.t, tab.s_cache, has_gate=True)
     assert cev_hip.AttnPlan(d, tab).n_splits == 2
-    # f32 chunks are long: 24 items of 12 chunks (12 x 32-token blocks after a
-    # 256-token prefix) take parts of 2 chunks; bf16 parts stay >= 4 chunks
+    # f32 key tiles are MFMA-heavy: 12 x 32-token blocks after a 256-token
+    # prefix (3 full tiles x 8 KV heads, at most half a round) get half-full
+    # tiles, 6 x 8 items, whose 12-chunk key streams split into 5 parts (one
+    # round); the same table in bf16 keeps full tiles
     tab = cev_hip.BlockTable.from_rows(12, 32, 256, causal=True)
     d = cev_hip.attn_desc(CEV_F32, 16, 8, 128, tab.t, tab.s_cache)
-    assert cev_hip.AttnPlan(d, tab).n_splits == 6
+    p = cev_hip.AttnPlan(d, tab)
+    assert p.n_tiles == 6 and p.n_splits == 5
+    d = cev_hip.attn_desc(CEV_BF16, 16, 8, 128, tab.t, tab.s_cache)
+    assert cev_hip.AttnPlan(d, tab).n_tiles == 3
     d = cev_hip.attn_desc(CEV_BF16, 16, 8, 128, tab.t, tab.s_cache)
     assert cev_hip.AttnPlan(d, tab).n_splits == 1
 
