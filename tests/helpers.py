@@ -42,6 +42,16 @@ class OracleLayer:
         self.v = v
         self.gate = q[:, :, d:] if w.gated else None
         self.pk, self.pv = pk, pv
+        self._masks = {}
+
+    def mask(self, b: int) -> np.ndarray:
+        """Additive mask of block b, built once (an 8192-token bidirectional
+        mask takes seconds)."""
+        if b not in self._masks:
+            w, orc, L = self.w, self.orc, self.w.blocks[b]
+            self._masks[b] = (orc.branch_mask(L, w.prefix) if w.causal else
+                              orc.bidirectional_mask(L, [w.lengths[b]])[0])
+        return self._masks[b]
 
     def block(self, b: int, rows=None, f64: bool = False):
         """Attention output (L, hq, d) of block b (rows=(r0, n) within it)."""
@@ -54,10 +64,7 @@ class OracleLayer:
         if w.prefix:
             kb = np.concatenate([self.pk, kb], axis=1)
             vb = np.concatenate([self.pv, vb], axis=1)
-        if w.causal:
-            mask = orc.branch_mask(L, w.prefix)
-        else:
-            mask = orc.bidirectional_mask(L, [w.lengths[b]])[0]
+        mask = self.mask(b)
         if f64:
             out = orc.attend_f64(qb, kb, vb, mask, rows=rows)[0].transpose(1, 0, 2)
         else:

@@ -2,10 +2,11 @@
 
 Bars (from the path's contract): attention output max |delta| <= 1e-5 in f32
 and <= 2e-2 in bf16 against the candle-op restatement on identical seeded
-inputs.  The QK-norm + RoPE prologue is checked bit for bit.  At full sizes
-the oracle runs on sampled blocks (rows are independent) and size-independent
-properties (packed == each block alone, poisoned keys, equivariances) cover
-the rest.
+inputs.  The QK-norm + RoPE prologue is checked bit for bit.  c1, c3 and c5a
+are compared in full, and c4's 8192-token row against the candle-op
+restatement in full; the f64 textbook covers every c1 and c5a block, three c3
+blocks and 512 c4 rows.  Size-independent properties (packed == each block
+alone, poisoned keys, equivariances) cover the rest.
 """
 import numpy as np
 import pytest
@@ -73,42 +74,48 @@ def test_c3_bf16_sampled_blocks(gpu, orc):
     _check_blocks(gl, ol, [0, 37, 63], BF16_TOL)
 
 
-def test_c3_bf16_every_block_one_kv_group(gpu, orc):
-    """All 64 blocks of the full c3 layer for one KV-head group (KV head 5,
-    query heads 20..23) against the oracle over [prefix || block]."""
+def test_c3_bf16_every_block_every_head(gpu, orc):
+    """All 64 blocks and all 32 query heads of the full c3 layer against the
+    candle-op oracle over [prefix || block] (the f64 textbook check runs on
+    the sampled blocks above)."""
     import torch
     w = configs.c3()
-    kvh, g = 5, w.hq // w.hkv
-    heads = slice(kvh * g, (kvh + 1) * g)
-    _say(f"test c3 every block: kv head {kvh}, query heads {heads.start}..{heads.stop - 1}")
+    _say(f"test c3 every block: {len(w.blocks)} blocks x {w.hq} heads")
     gl = GpuLayer(w, gpu)
     ol = OracleLayer(orc, w, gl.np_inputs)
     gl.forward()
     torch.cuda.synchronize()
-    out = to_np(gl.out)[:, heads]
+    out = to_np(gl.out)
     worst = 0.0
-    pk, pv = ol.pk[kvh:kvh + 1], ol.pv[kvh:kvh + 1]
     for b in range(len(w.blocks)):
         r0, L = int(w.block_starts()[b]), w.blocks[b]
-        qb = np.ascontiguousarray(ol.q[r0:r0 + L, heads].transpose(1, 0, 2))
-        kb = np.concatenate([pk, ol.k[r0:r0 + L, kvh:kvh + 1].transpose(1, 0, 2)], axis=1)
-        vb = np.concatenate([pv, ol.v[r0:r0 + L, kvh:kvh + 1].transpose(1, 0, 2)], axis=1)
-        want = orc.attend(qb, kb, vb, orc.branch_mask(L, w.prefix), True)[0].transpose(1, 0, 2)
-        worst = max(worst, float(np.abs(out[r0:r0 + L] - want).max()))
-    _say(f"  64 blocks: max|d| {worst:.3g}")
+        got = out[r0:r0 + L]
+        assert np.isfinite(got).all()
+        worst = max(worst, float(np.abs(got - ol.block(b)).max()))
+    _say(f"  {len(w.blocks)} blocks: max|d| {worst:.3g}")
     assert worst <= BF16_TOL
 
 
-def test_c4_bidirectional_gated_sampled_rows(gpu, orc):
+def test_c4_bidirectional_gated_full_row(gpu, orc):
+    """Every row and head of the 8192-token bidirectional gated row against
+    the candle-op oracle; eight 64-row windows (the first and the last rows
+    among them) also against the f64 textbook."""
+    import torch
     w = configs.c4()
     _say(f"test c4: t={w.t} hq={w.hq} hkv={w.hkv} d={w.d}")
     gl = GpuLayer(w, gpu)
     ol = OracleLayer(orc, w, gl.np_inputs)
     gl.forward()
+    torch.cuda.synchronize()
     assert np.array_equal(to_np(gl.q), ol.q)
     assert np.array_equal(to_np(gl.k), ol.k)
-    for r0 in (0, 4000, 8160):
-        _check_blocks(gl, ol, [0], BF16_TOL, rows=(r0, 32))
+    got = to_np(gl.out)
+    assert np.isfinite(got).all()
+    err = float(np.abs(got - ol.block(0)).max())
+    _say(f"c4 all {w.t} rows: max|d| vs candle-op oracle {err:.3g}")
+    assert err <= BF16_TOL
+    for r0 in (0, 1000, 2047, 3333, 4000, 5555, 7000, 8128):
+        _check_blocks(gl, ol, [0], BF16_TOL, rows=(r0, 64))
 
 
 def _d3_check(gpu, orc, w, tol):
@@ -186,7 +193,7 @@ def test_c5_gated_rows_continue_prefix(gpu, orc):
     gl = GpuLayer(w, gpu, table=tab)
     ol = OracleLayer(orc, w, gl.np_inputs)
     gl.forward()
-    _check_blocks(gl, ol, [0, 5, 31], BF16_TOL)
+    _check_blocks(gl, ol, range(len(w.blocks)), BF16_TOL)
 
 
 SMALL = [
