@@ -1074,6 +1074,292 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
     }
 }
 
+// --------------------------------------------------------------------------
+// bf16, d = 256: the sequential chunk body of attn_kernel_seq (score, softmax,
+// then multiply into O) fed the way attn_kernel_pipe is fed.  32-key chunks
+// go from HBM straight into a ring of kBuf LDS buffers (buffer_load ... lds),
+// kAhead chunks in flight ahead of the one being scored, so no register
+// holds staged K/V and a chunk's fetch latency is spread over three chunk
+// bodies instead of one.  Rows are 512 bytes, unpadded, with the 16-byte
+// column blocks permuted for conflict-free operand reads:
+//   K: block c of row r at slot c ^ (r & 15)     (ds_read_b128, one key row
+//      per lane: 16 rows cover every bank once)
+//   V: block c of row r at slot c ^ 4(r & 3)     (ds_read_b64_tr_b16, four
+//      rows x four blocks per 16 lanes)
+// Bit 4 of a block index is never permuted, so the operand read addresses
+// of the upper 128 head-dim values are the lower ones' plus 256 bytes.
+namespace wide {
+constexpr int kBuf = 4;
+constexpr int kAhead = kBuf - 1;
+constexpr int kKeys = 32;                      // keys per chunk
+constexpr int kRowBytes = 512;                 // one bf16 row of d = 256
+constexpr int kTileBytes = kKeys * kRowBytes;  // K (or V) of one chunk
+constexpr int kVBase = kBuf * kTileBytes;      // the K tiles, then the V tiles
+constexpr int kLoadsPerChunk = 4;              // buffer_load ... lds per wave per chunk
+constexpr int kKPF = 3;                        // K fragments read ahead of their MFMA
+constexpr int kVPF = 3;                        // V fragments read ahead of their MFMA
+static_assert(kAttnWaves * 4 == kKeys, "each wave fetches four K rows and four V rows");
+
+__device__ __forceinline__ int k_slot(int blk, int row) { return blk ^ (row & 15); }
+__device__ __forceinline__ int v_slot(int blk, int row) { return blk ^ ((row & 3) << 2); }
+
+// lgkmcnt of QK unit st (16 units, K reads kKPF ahead) and PV unit j (16
+// units, two reads per V fragment, kVPF fragments ahead): the LDS reads
+// issued after the one the unit needs.
+constexpr int wait_k(int st) { return (15 - st) < kKPF - 1 ? 15 - st : kKPF - 1; }
+constexpr int wait_v(int j) { return 2 * ((15 - j) < kVPF - 1 ? 15 - j : kVPF - 1); }
+}  // namespace wide
+
+template <typename T, int D>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) {
+  using F = Frag<T, D>;
+  using P = typename F::P;
+  static_assert(sizeof(T) == 2 && D == 256 && F::BN == wide::kKeys && kAttnWaves == 8, "sized for bf16, d = 256");
+  static_assert(F::NQK == 16 && F::NPV == 16, "unit layout below");
+  using namespace wide;
+  using pipe::i32x2;
+  using pipe::KFrag;
+  constexpr int NDT = D / 32;
+  __shared__ __align__(16) char lds[2 * kBuf * kTileBytes];
+
+  if (!plan_ok(a)) {
+    poison_output<T, D>(a);
+    return;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform_i32(tid >> 6);
+  const int n = lane & 31, u = lane >> 5;
+  const int kvh = blockIdx.x % a.hkv;
+  const int item = blockIdx.x / a.hkv;
+  const int tile = item / a.n_splits, part = item % a.n_splits;
+  const cev_plan_header* ph = (const cev_plan_header*)a.plan;
+  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[2 * tile];
+  const int n_chunks = ((const int4*)(a.plan + ph->tiles_off))[2 * tile + 1].x;
+  const int4* segs = (const int4*)(a.plan + ph->segs_off) + td.z;
+  const int nseg = td.w;
+  const int4* rows = (const int4*)(a.plan + ph->rows_off);
+  // Query slot (wave, n) holds row slot / g of the tile, query head slot % g;
+  // a wave with no valid row skips the MFMA work and still fetches its rows.
+  const int slot = wave * 32 + n;
+  const int gi = slot % a.g;
+  const int head = kvh * a.g + gi;
+  const int rit = slot / a.g;
+  const bool row_ok = rit < td.y && td.x + rit < a.t;
+  const int row = row_ok ? td.x + rit : 0;
+  const bool wave_active = (wave * 32) / a.g < td.y;
+  const float c = a.scale_log2;
+
+  F fr;
+  fr.load_q((const T*)a.q + (int64_t)row * a.q_st + (int64_t)head * a.q_sh, row_ok, u);
+  int4 rv = rows[row];
+  if (!row_ok) rv = make_int4(0, 0, -1, 0);
+
+  f32x16 o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
+  float m_run = -1e30f, l_run = 0.0f;
+
+  const int c0 = (int)((int64_t)part * n_chunks / a.n_splits);
+  const int c1 = (int)((int64_t)(part + 1) * n_chunks / a.n_splits);
+  const int nc = c1 - c0;
+  ChunkCursor<kKeys> cursor{segs, nseg, a.s_cache, a.t, 0, 0, make_int4(0, 0, 0, 0)};
+  cursor.seek(c0);
+  if (nc > 0 && cursor.valid()) {
+    KvSource<T> kvs;
+    kvs.init(a, kvh);
+
+    // Per-lane byte offsets of the operand reads (V's include kVBase), for
+    // head-dim blocks 0..15; the upper half adds 256 bytes as an immediate,
+    // and so do the buffer and key row, so every offset field stays below
+    // 64 KB.
+    int koff[8], voff[4];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) koff[st] = n * kRowBytes + (k_slot(2 * st + u, n) << 4);
+    {
+      const int i = lane & 15, g16 = (lane >> 4) & 1, rr = i >> 2;
+      const int blk = 2 * g16 + ((i & 3) >> 1);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) voff[dt] = kVBase + (4 * u + rr) * kRowBytes + (v_slot(4 * dt + blk, rr) << 4) + 8 * (i & 1);
+    }
+    const int lds_base = (int)(size_t)(const __attribute__((address_space(3))) char*)lds;
+    // K fragment st (head-dim values 16 st + 8u ..) of the chunk in buffer BUF.
+    auto k_issue = [&](auto buf_c, auto st_c) {
+      constexpr int BUF = decltype(buf_c)::value, ST = decltype(st_c)::value;
+      return pipe::read_b128<BUF * kTileBytes + 256 * (ST >> 3)>(lds_base + koff[ST & 7]);
+    };
+    // V^T fragment j (keys 16 (j / 8) .., head-dim slice j % 8): the transpose
+    // reads of rows r and r + 8.
+    struct VFrag {
+      i32x2 lo, hi;
+    };
+    auto v_issue = [&](auto buf_c, auto j_c) {
+      constexpr int BUF = decltype(buf_c)::value, J = decltype(j_c)::value;
+      constexpr int OFF = BUF * kTileBytes + 16 * (J / NDT) * kRowBytes + 256 * ((J % NDT) >> 2);
+      const int va = lds_base + voff[(J % NDT) & 3];
+      return VFrag{pipe::read_tr<OFF>(va), pipe::read_tr<OFF + 8 * kRowBytes>(va)};
+    };
+
+    // Chunk ch into buffer buf: wave w fetches K and V rows 4w .. 4w + 3, two
+    // rows (1 KB) per instruction; rows past the chunk's last valid key read
+    // as zero.
+    auto fetch = [&](const Chunk& ch, int buf) {
+      __amdgpu_buffer_rsrc_t rk, rvs;
+      int kr, vr;
+      kvs.rsrc(ch, rk, rvs, kr, vr);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int krow = 4 * wave + 2 * r + (lane >> 5), blk = lane & 31;
+        const int kdst = buf * kTileBytes + (4 * wave + 2 * r) * kRowBytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(lds + kdst), 16,
+                                                 krow * kr + (k_slot(blk, krow) << 4), 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rvs, (__attribute__((address_space(3))) void*)(lds + kVBase + kdst), 16,
+                                                 krow * vr + (v_slot(blk, krow) << 4), 0, 0, 0);
+      }
+    };
+
+    // Stale LDS must hold finite values (a masked key's V row is multiplied
+    // by p = 0): zero every buffer once, waiting for LDS writes only.
+    for (int i = tid; i < 2 * kBuf * kTileBytes / 16; i += kAttnWaves * 64) *(f32x4*)(lds + 16 * i) = f32x4{};
+    pipe::lds_barrier();
+
+    int produced = 0;
+    auto next_chunk = [&]() {
+      Chunk ch{0, 0, 0};
+      if (produced < nc) {
+        if (produced > 0) cursor.next();
+        ch = cursor.here();
+      }
+      ++produced;
+      return ch;
+    };
+    Chunk chs[kAhead + 1];
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) {
+      chs[k] = next_chunk();
+      fetch(chs[k], k);
+    }
+    pipe::wait_vmcnt<kLoadsPerChunk * (kAhead - 1)>();  // chunk 0 landed
+    __builtin_amdgcn_s_barrier();
+
+    // Iteration i scores the chunk in buffer B (chunk i of the part), after
+    // fetching chunk i + kAhead into the buffer chunk i - 1 used; before its
+    // barrier it waits for chunk i + 1 to land.
+    auto step = [&](auto buf_tag) {
+      constexpr int B = decltype(buf_tag)::value;
+      using B_c = std::integral_constant<int, B>;
+      chs[kAhead] = next_chunk();
+      fetch(chs[kAhead], (B + kAhead) % kBuf);
+      const Chunk ch = chs[0];
+      if (wave_active) {
+        f32x16 s = {};
+        KFrag kf[kKPF];
+        static_for<kKPF>([&](auto f_c) { kf[decltype(f_c)::value] = k_issue(B_c{}, f_c); });
+        static_for<F::NQK>([&](auto st_c) {
+          constexpr int st = decltype(st_c)::value;
+          pipe::wait_b128<wait_k(st)>(kf[st % kKPF]);
+          fr.qk_mfma(__builtin_bit_cast(bf16x8, kf[st % kKPF]), st, s);
+          if constexpr (st + kKPF < F::NQK) kf[st % kKPF] = k_issue(B_c{}, std::integral_constant<int, st + kKPF>{});
+        });
+        // the first V fragments load under the softmax
+        VFrag vf[kVPF];
+        static_for<kVPF>([&](auto j_c) { vf[decltype(j_c)::value] = v_issue(B_c{}, j_c); });
+        if (ch.local != 0 || ch.nvalid < kKeys) {
+          // Branch-free on purpose (see attn_kernel_seq).
+          const bool all_rows = ch.local == 0;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kk = 8 * (i >> 2) + 4 * u + (i & 3);
+            const int key = ch.key0 + kk;
+            const bool vis = (kk < ch.nvalid) & (all_rows | ((key >= rv.x) & (key < rv.y)) | (key == rv.z));
+            s[i] = vis ? s[i] : -INFINITY;
+          }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        const float m_cand = pair_max(mx) * c;
+        const bool grow = m_cand > m_run + kRescale;
+        if (__ballot(grow)) {
+          const float m_new = grow ? m_cand : m_run;
+          const float alpha = fast_exp2(m_run - m_new);
+          m_run = m_new;
+          l_run *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = fast_exp2(__builtin_fmaf(s[i], c, -m_run));
+        P p;
+        float rs = 0.0f;
+        F::make_p(s, p, rs);
+        static_for<F::NPV>([&](auto j_c) {
+          constexpr int j = decltype(j_c)::value;
+          VFrag& f = vf[j % kVPF];
+          pipe::wait_tr<wait_v(j)>(f.lo, f.hi);
+          const bf16x4 lo = __builtin_bit_cast(bf16x4, f.lo), hi = __builtin_bit_cast(bf16x4, f.hi);
+          F::pv_mfma(bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, j, p, o);
+          if constexpr (j + kVPF < F::NPV) f = v_issue(B_c{}, std::integral_constant<int, j + kVPF>{});
+        });
+        l_run += rs;
+      }
+      pipe::wait_vmcnt<kLoadsPerChunk * (kAhead - 1)>();  // chunk i + 1 landed
+      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int k = 0; k < kAhead; ++k) chs[k] = chs[k + 1];
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    static_assert(kBuf == 4, "the unrolled loop below walks four buffers");
+    for (int ci = 0; ci < nc; ci += kBuf) {
+      step(I0{});
+      if (ci + 1 >= nc) break;
+      step(I1{});
+      if (ci + 2 >= nc) break;
+      step(I2{});
+      if (ci + 3 >= nc) break;
+      step(I3{});
+    }
+    // Fetches past the part's end read no memory but still write zeros into
+    // LDS: drain them before the workgroup exits.
+    pipe::wait_vmcnt<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+
+  const float l = pair_sum(l_run);
+  if (!row_ok) return;
+  if (a.n_splits > 1) {
+    float* rec = a.ws + (((int64_t)row * a.hq + head) * a.n_splits + part) * cev_attn_partial_floats(D);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = dt * 32 + 8 * q4 + 4 * u;
+        *(f32x4*)(rec + d) = f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
+      }
+    if (u == 0) *(f32x4*)(rec + D) = f32x4{m_run, l, 0.0f, 0.0f};
+    return;
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh : nullptr;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = dt * 32 + 8 * q4 + 4 * u;
+      float v[4], gv[4];
+      if (gp) load_vec4<T>(gp + d, gv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x = o[dt][4 * q4 + e] * inv;
+        if (gp) x = gate_value(x, gv[e], true);
+        v[e] = x;
+      }
+      store_vec4<T>(op + d, v);
+    }
+}
+
 // Combines the parts of split tiles: for each (row, head),
 //   M = max_s m_s,  L = sum_s 2^(m_s - M) l_s,  O = sum_s 2^(m_s - M) O_s / L.
 // One wave per (row, head), kMergeWaves per workgroup.  Lane l reads the
@@ -1175,6 +1461,8 @@ int32_t launch(const AttnArgs& a, hipStream_t stream) {
   if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "grid of %lld workgroups is too large", (long long)grid);
   if constexpr (sizeof(T) == 2 && D == 128)
     hipLaunchKernelGGL((attn_kernel_pipe<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
+  else if constexpr (sizeof(T) == 2 && D == 256)
+    hipLaunchKernelGGL((attn_kernel_wide<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
   else
     hipLaunchKernelGGL((attn_kernel_seq<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
   hipError_t e = hipGetLastError();
