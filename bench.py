@@ -475,7 +475,8 @@ def main():
 
     dtype = "bf16" if w.bf16 else "f32"
     flops = w.useful_flops()
-    kernel = "attn_kernel_pipe<bf16,128>" if (w.bf16 and w.d == 128) else f"attn_kernel_seq<{dtype},{w.d}>"
+    kernel = {(True, 128): "attn_kernel_pipe<bf16,128>", (True, 256): "attn_kernel_wide<bf16,256>"}.get(
+        (w.bf16, w.d), f"attn_kernel_seq<{dtype},{w.d}>")
     roof = roofline(flops, w.alg_bytes(), k2_ms, dtype, kernel, traffic_from_profiles(w.name))
 
     res = {

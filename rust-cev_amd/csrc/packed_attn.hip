@@ -14,8 +14,9 @@
 //     O rescaled only when a row max grows by more than 2^kRescale;
 //   - O^T = V^T . P^T accumulates on MFMA with P kept in registers as the B
 //     operand (its K slots follow the S^T register order);
-//   - K/V key tiles are double-buffered in LDS: the next tile's global loads
-//     are in flight while the current one is scored;
+//   - K/V key tiles stream through LDS ahead of the one being scored: bf16
+//     chunks go from HBM straight into a four-deep LDS ring (buffer_load ...
+//     lds), f32 chunks are double-buffered through registers;
 //   - the key ranges a tile visits come from the plan: spans are unmasked,
 //     local keys are masked per row from the row's [lo, hi) + diag;
 //   - blockIdx -> (tile, part, kv head) with the kv head fastest, so the
