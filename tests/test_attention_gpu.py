@@ -255,7 +255,27 @@ def test_packed_equals_each_block_alone_on_gpu(gpu):
         assert np.array_equal(to_np(alone), packed[r0:r0 + L])
 
 
-def test_poisoned_invisible_keys_are_never_read(gpu, orc):
+def test_packed_rows_equal_each_row_alone_d256(gpu):
+    """The same for the d = 256 kernel on the gated-rows layer: unsplit, each
+    of the 32 rows run alone over [prefix || row] matches its packed rows
+    bit for bit."""
+    w = configs.c5_attention()
+    tab = cev_hip.BlockTable.from_rows(len(w.blocks), w.blocks[0], w.prefix, causal=True)
+    gl = GpuLayer(w, gpu, table=tab)
+    gl.forward()
+    packed = cev_hip.packed_attention(gl.q, gl.k, gl.v, tab, k_cache=gl.pk, v_cache=gl.pv, max_splits=1)
+    packed = to_np(packed)
+    assert np.isfinite(packed).all()
+    for b in (0, 13, 31):
+        r0, L = int(w.block_starts()[b]), w.blocks[b]
+        one = cev_hip.BlockTable.from_rows(1, L, w.prefix, causal=True)
+        alone = cev_hip.packed_attention(gl.q[r0:r0 + L], gl.k[r0:r0 + L], gl.v[r0:r0 + L], one, k_cache=gl.pk, v_cache=gl.pv,
+                                         max_splits=1)
+        assert np.array_equal(to_np(alone), packed[r0:r0 + L])
+
+
+@pytest.mark.parametrize("d", [128, 256])
+def test_poisoned_invisible_keys_are_never_read(gpu, orc, d):
     """A row never reads another plan's K/V.  Per plan p: NaN in every other
     plan's past (cache keys), in the K/V of every new token another plan
     owns, and in keys past the end of the cache must leave plan p's rows
@@ -272,7 +292,7 @@ def test_poisoned_invisible_keys_are_never_read(gpu, orc):
     t, s = ep["n"], ep["past_total"]
     owner = ep["owner"]
     past_off = np.cumsum([0] + [p_[0] for p_ in plans])
-    hq, hkv, d = 16, 4, 128
+    hq, hkv = 16, 4
     rng = np.random.default_rng(5)
     q = orc.round_bf16(rng.standard_normal((t, hq, d)).astype(np.float32))
     kn = orc.round_bf16(rng.standard_normal((t, hkv, d)).astype(np.float32))
@@ -299,7 +319,7 @@ def test_poisoned_invisible_keys_are_never_read(gpu, orc):
                                              k_cache=to_dev(kcp, bf, gpu)[:, :s], v_cache=to_dev(vcp, bf, gpu)[:, :s]))
         torch.cuda.synchronize()
         mine = owner == p
-        _say(f"poisoned run for plan {p}: {int(mine.sum())} rows checked")
+        _say(f"poisoned run for plan {p}, d={d}: {int(mine.sum())} rows checked")
         assert np.isfinite(got[mine]).all()
         assert np.array_equal(got[mine], clean[mine])
 
