@@ -1105,10 +1105,41 @@ __device__ __forceinline__ int k_slot(int blk, int row) { return blk ^ (row & 15
 __device__ __forceinline__ int v_slot(int blk, int row) { return blk ^ ((row & 3) << 2); }
 
 // lgkmcnt of QK unit st (16 units, K reads kKPF ahead) and PV unit j (16
-// units, two reads per V fragment, kVPF fragments ahead): the LDS reads
-// issued after the one the unit needs.
+// units, two reads per V fragment, kVPF fragments ahead; the last kKPF units
+// also issue the next chunk's first K reads): the LDS reads issued after
+// the one the unit needs.  The PV counts replay one body's issue order.
 constexpr int wait_k(int st) { return (15 - st) < kKPF - 1 ? 15 - st : kKPF - 1; }
-constexpr int wait_v(int j) { return 2 * ((15 - j) < kVPF - 1 ? 15 - j : kVPF - 1); }
+struct PvWaits {
+  int w[16];
+};
+constexpr PvWaits pv_waits() {
+  PvWaits r{};
+  int vhi[16] = {};
+  int pos = 0;
+  for (int j = 0; j < kVPF; ++j) {
+    vhi[j] = pos + 1;
+    pos += 2;
+  }
+  for (int j = 0; j < 16; ++j) {
+    r.w[j] = pos - vhi[j] - 1;
+    if (j + kVPF < 16) {
+      vhi[j + kVPF] = pos + 1;
+      pos += 2;
+    }
+    if (j >= 16 - kKPF) ++pos;
+  }
+  return r;
+}
+constexpr PvWaits kPvWaits = pv_waits();
+constexpr int wait_v(int j) { return kPvWaits.w[j]; }
+constexpr bool pv_waits_ok() {
+  for (int j = 0; j < 16; ++j)
+    if (kPvWaits.w[j] < 0 || kPvWaits.w[j] > 15) return false;
+  return true;
+}
+static_assert(pv_waits_ok(), "lgkmcnt range");
+static_assert(kVPF == 3 && kKPF == 3 ? (wait_v(0) == 4 && wait_v(12) == 4 && wait_v(13) == 4 && wait_v(14) == 3 && wait_v(15) == 2) : true,
+              "wait counts at three fragments ahead");
 }  // namespace wide
 
 template <typename T, int D>
@@ -1238,12 +1269,18 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
       chs[k] = next_chunk();
       fetch(chs[k], k);
     }
-    pipe::wait_vmcnt<kLoadsPerChunk * (kAhead - 1)>();  // chunk 0 landed
+    pipe::wait_vmcnt<kLoadsPerChunk * (kAhead - 2)>();  // chunks 0 and 1 landed
     __builtin_amdgcn_s_barrier();
+    using I0 = std::integral_constant<int, 0>;
+    // K reads in flight into the next body: the first body's are issued
+    // here, every later body's in the previous body's last P.V units.
+    KFrag kf[kKPF];
+    if (wave_active) static_for<kKPF>([&](auto f_c) { kf[decltype(f_c)::value] = k_issue(I0{}, f_c); });
 
     // Iteration i scores the chunk in buffer B (chunk i of the part), after
     // fetching chunk i + kAhead into the buffer chunk i - 1 used; before its
-    // barrier it waits for chunk i + 1 to land.
+    // barrier it waits for chunk i + 2 to land (the next iteration reads
+    // chunk i + 2's first K fragments).
     auto step = [&](auto buf_tag) {
       constexpr int B = decltype(buf_tag)::value;
       using B_c = std::integral_constant<int, B>;
@@ -1252,8 +1289,6 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
       const Chunk ch = chs[0];
       if (wave_active) {
         f32x16 s = {};
-        KFrag kf[kKPF];
-        static_for<kKPF>([&](auto f_c) { kf[decltype(f_c)::value] = k_issue(B_c{}, f_c); });
         static_for<F::NQK>([&](auto st_c) {
           constexpr int st = decltype(st_c)::value;
           pipe::wait_b128<wait_k(st)>(kf[st % kKPF]);
@@ -1299,15 +1334,19 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
           const bf16x4 lo = __builtin_bit_cast(bf16x4, f.lo), hi = __builtin_bit_cast(bf16x4, f.hi);
           F::pv_mfma(bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, j, p, o);
           if constexpr (j + kVPF < F::NPV) f = v_issue(B_c{}, std::integral_constant<int, j + kVPF>{});
+          // the next body's first K reads (chunk i + 1, landed before the
+          // previous barrier; past the part's end they read a stale buffer
+          // and are never used)
+          if constexpr (j >= F::NPV - kKPF)
+            kf[j - (F::NPV - kKPF)] = k_issue(std::integral_constant<int, (B + 1) % kBuf>{}, std::integral_constant<int, j - (F::NPV - kKPF)>{});
         });
         l_run += rs;
       }
-      pipe::wait_vmcnt<kLoadsPerChunk * (kAhead - 1)>();  // chunk i + 1 landed
+      pipe::wait_vmcnt<kLoadsPerChunk * (kAhead - 2)>();  // chunk i + 2 landed
       __builtin_amdgcn_s_barrier();
 #pragma unroll
       for (int k = 0; k < kAhead; ++k) chs[k] = chs[k + 1];
     };
-    using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
