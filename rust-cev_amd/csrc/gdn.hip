@@ -1155,8 +1155,19 @@ __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(4)
 }
 
 // ---------------------------------------------------------------------------
-// norm: one wave per (row, token, value head): y = core / sqrt(mean core^2
-// + eps) * w * silu(z), cast to the model dtype (qwen35.rs:447-451).
+// norm: y = core / sqrt(mean core^2 + eps) * w * silu(z), cast to the model
+// dtype (qwen35.rs:447-451), all in f32.  The division by the row's norm is
+// one reciprocal per row and silu(z) = z / (1 + e^-z) takes the hardware
+// exp2 and reciprocal: a few f32 ulps from the reference's op sequence,
+// which the output's tolerance covers, for a third of the VALU work (the
+// kernel is otherwise bound by it, not by its 134 MB of traffic on a
+// 4096-token row).
+__device__ __forceinline__ float gated_norm(float c, float inv, float w, float z) {
+  const float ez = __builtin_amdgcn_exp2f(z * -1.4426950408889634f);
+  return c * inv * w * (z * __builtin_amdgcn_rcpf(1.0f + ez));
+}
+
+// One wave per (row, token, value head).
 template <typename T>
 __global__ __launch_bounds__(256) void gdn_norm_kernel(GdnArgs g) {
   const int lane = threadIdx.x & 63;
@@ -1170,17 +1181,13 @@ __global__ __launch_bounds__(256) void gdn_norm_kernel(GdnArgs g) {
   float s = cv.x * cv.x + cv.y * cv.y;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  const float den = sqrtf(s / (float)kD + g.eps);
+  const float inv = 1.0f / sqrtf(s / (float)kD + g.eps);
   const T* zr = (const T*)g.z + r * g.z_sb + (int64_t)t * g.z_st + h * kD + 2 * lane;
   T* yr = (T*)g.y + r * g.y_sb + (int64_t)t * g.y_st + h * kD + 2 * lane;
   const float2 wv = *(const float2*)(g.norm_w + 2 * lane);
   const float c2[2] = {cv.x, cv.y}, w2[2] = {wv.x, wv.y};
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const float zz = to_f(zr[e]);
-    const float gate = zz / (1.0f + expf(-zz));
-    yr[e] = from_f<T>(c2[e] / den * w2[e] * gate);
-  }
+  for (int e = 0; e < 2; ++e) yr[e] = from_f<T>(gated_norm(c2[e], inv, w2[e], to_f(zr[e])));
 }
 
 // The same with 16 lanes per (row, token, value head), 8 elements each:
@@ -1207,13 +1214,10 @@ __global__ __launch_bounds__(256) void gdn_norm_vec_kernel(GdnArgs g) {
   float s = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) s += cv[e] * cv[e];
-  const float den = sqrtf(row16_sum(s) / (float)kD + g.eps);
+  const float inv = 1.0f / sqrtf(row16_sum(s) / (float)kD + g.eps);
   float y[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float gate = zv[e] / (1.0f + expf(-zv[e]));
-    y[e] = cv[e] / den * wv[e] * gate;
-  }
+  for (int e = 0; e < 8; ++e) y[e] = gated_norm(cv[e], inv, wv[e], zv[e]);
   if (item < n_items) store8<T>((T*)g.y + r * g.y_sb + (int64_t)t * g.y_st + h * kD + 8 * sub, y);
 }
 
