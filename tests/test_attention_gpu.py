@@ -449,6 +449,45 @@ def test_million_key_prefix_many_parts(gpu):
     assert worst <= BF16_TOL
 
 
+def test_long_prefix_many_parts_d256(gpu):
+    """The d = 256 kernel and merge with many parts: a 2^17-key cached prefix
+    with one 16-token causal block, g = 4.  Sampled rows and heads are held
+    to exact attention in f64 over every key (planted keys aligned with
+    each sampled query carry most of the weight), and the split result to
+    the unsplit one."""
+    import torch
+    P, t, hq, hkv, d = 1 << 17, 16, 16, 4, 256
+    _say(f"test long prefix d=256: P={P} t={t} hq={hq} hkv={hkv}")
+    rng = np.random.default_rng(21)
+    f = lambda *shape: torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(gpu).to(torch.bfloat16)  # noqa: E731
+    q, kn, vn = f(t, hq, d), f(t, hkv, d), f(t, hkv, d)
+    kc, vc = f(hkv, P, d), f(hkv, P, d)
+    samples = [(0, 0, (3, 65_537, P - 2)), (9, 6, (40_000, 100_001, P - 7)), (15, 15, (0, 77_777, 131_000))]
+    for i, h, where in samples:
+        for pos in where:
+            kc[h // (hq // hkv), pos] = (0.75 * q[i, h].float()).to(torch.bfloat16)
+    tab = cev_hip.BlockTable.from_rows(1, t, P, causal=True)
+    attn = cev_hip.PackedAttention(q, kn, tab, k_cache=kc, s_cache=P, v_new=vn, v_cache=vc)
+    assert attn.plan.n_splits >= 16, attn.plan.n_splits
+    out = to_np(attn(q, kn, vn, kc, vc))
+    whole = to_np(cev_hip.packed_attention(q, kn, vn, tab, k_cache=kc, v_cache=vc, max_splits=1))
+    assert np.isfinite(out).all()
+    assert np.abs(whole - out).max() <= 2 * 2.0 ** -7
+    qn = to_np(q).astype(np.float64)
+    worst = 0.0
+    for i, h, _ in samples:
+        kvh = h // (hq // hkv)
+        keys = P + i + 1
+        k_all = np.concatenate([to_np(kc)[kvh], to_np(kn)[:, kvh]]).astype(np.float64)[:keys]
+        v_all = np.concatenate([to_np(vc)[kvh], to_np(vn)[:, kvh]]).astype(np.float64)[:keys]
+        sc = k_all @ qn[i, h] / np.sqrt(d)
+        pr = np.exp(sc - sc.max())
+        ref = (pr @ v_all) / pr.sum()
+        worst = max(worst, float(np.abs(out[i, h] - ref).max()))
+    _say(f"  parts {attn.plan.n_splits}, max|d| vs exact f64 {worst:.3g}, split vs whole {np.abs(whole - out).max():.3g}")
+    assert worst <= BF16_TOL
+
+
 def test_split_f32_matches_unsplit(gpu):
     w = configs.c1()
     gl = GpuLayer(w, gpu)
