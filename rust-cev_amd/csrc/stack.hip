@@ -35,6 +35,7 @@
 // bounds the top) and m in [2^-20, 2^20].  A row outside that range takes
 // the IEEE division; copysign keeps the sign of -0 / m.
 #include <algorithm>
+#include <type_traits>
 
 #include "cev_device.h"
 #include "cev_internal.h"
@@ -205,7 +206,12 @@ __device__ __forceinline__ int wave_min_i32(int v) {
 }
 
 // One wave per row, lane l holding chunks l, l + 64, ... (NCH at most).
-template <typename T, int NCH>
+// Every lane loads all NCH chunks of x, h and the weight at once (indices
+// clamped to the row, so the loads are unconditional and all in flight
+// together); chunks past the row are neither summed nor stored.  The
+// residual is a template parameter and the division path is chosen once
+// per row, so no branch sits inside the element loops.
+template <typename T, int NCH, bool RES>
 __global__ __launch_bounds__(kWaveNormRows * 64) void rms_norm_wave_kernel(NormArgs a) {
   constexpr bool BF = sizeof(T) == 2;
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -214,33 +220,33 @@ __global__ __launch_bounds__(kWaveNormRows * 64) void rms_norm_wave_kernel(NormA
   const int64_t r = (int64_t)blockIdx.x * kWaveNormRows + (threadIdx.x >> 6);
   if (r >= a.rows) return;
   const int nc = a.hidden / VEC;
-  u32x4 cx[NCH], ch[NCH];
+  u32x4 cx[NCH], ch[NCH], cw[NCH];
 #pragma unroll
   for (int b = 0; b < NCH; ++b) {
-    const int k = lane + 64 * b;
-    if (k < nc) {
-      cx[b] = *(const u32x4*)((const T*)a.x + r * a.x_st + k * VEC);
-      if (a.h) ch[b] = *(const u32x4*)((const T*)a.h + r * a.h_st + k * VEC);
-    }
+    const int k = min(lane + 64 * b, nc - 1);
+    cx[b] = *(const u32x4*)((const T*)a.x + r * a.x_st + k * VEC);
+    if constexpr (RES) ch[b] = *(const u32x4*)((const T*)a.h + r * a.h_st + k * VEC);
+    cw[b] = *(const u32x4*)((const T*)a.w + k * VEC);
   }
   float s = 0.0f;
   int me = 0;
 #pragma unroll
   for (int b = 0; b < NCH; ++b) {
     const int k = lane + 64 * b;
-    if (k < nc) {
-      float xs[VEC];
+    const bool in_row = k < nc;
+    float xs[VEC];
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) xs[j] = a.h ? rnd(elem<T>(cx[b], j) + elem<T>(ch[b], j)) : elem<T>(cx[b], j);
-      if (a.h) {
-        cx[b] = pack<T>(xs);
-        *(u32x4*)((T*)a.x_out + r * a.xo_st + k * VEC) = cx[b];
-      }
+    for (int j = 0; j < VEC; ++j) xs[j] = RES ? rnd(elem<T>(cx[b], j) + elem<T>(ch[b], j)) : elem<T>(cx[b], j);
+    if constexpr (RES) {
+      cx[b] = pack<T>(xs);
+      if (in_row) *(u32x4*)((T*)a.x_out + r * a.xo_st + k * VEC) = cx[b];
+    }
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        s = __builtin_fmaf(xs[j], xs[j], s);
-        me = min(me, __builtin_amdgcn_frexp_expf(xs[j]));
-      }
+    for (int j = 0; j < VEC; ++j) {
+      const float sj = __builtin_fmaf(xs[j], xs[j], s);
+      const int mj = min(me, __builtin_amdgcn_frexp_expf(xs[j]));
+      s = in_row ? sj : s;
+      me = in_row ? mj : me;
     }
   }
   s = wave_sum_f32(s);
@@ -248,29 +254,32 @@ __global__ __launch_bounds__(kWaveNormRows * 64) void rms_norm_wave_kernel(NormA
   const float m = rnd(sqrtf(s / (float)a.hidden + a.eps));
   const float y = 1.0f / m;
   const bool fast = me >= -95 && s <= 0x1p120f && m >= 0x1p-20f && m <= 0x1p20f;
+  auto norm_row = [&](auto fast_c) {
 #pragma unroll
-  for (int b = 0; b < NCH; ++b) {
-    const int k = lane + 64 * b;
-    if (k < nc) {
-      const u32x4 cw = *(const u32x4*)((const T*)a.w + k * VEC);
+    for (int b = 0; b < NCH; ++b) {
+      const int k = lane + 64 * b;
       float ys[VEC];
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         const float x = elem<T>(cx[b], j);
         float q;
-        if (fast) {
+        if constexpr (decltype(fast_c)::value) {
           const float q0 = x * y;
           q = __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, m, x), y, q0), q0);
         } else {
           q = x / m;
         }
-        float w = elem<T>(cw, j);
-        if (a.plus_one) w = rnd(w + 1.0f);
+        const float w0 = elem<T>(cw[b], j);
+        const float w = a.plus_one ? rnd(w0 + 1.0f) : w0;
         ys[j] = rnd(rnd(q) * w);
       }
-      *(u32x4*)((T*)a.y + r * a.y_st + k * VEC) = pack<T>(ys);
+      if (k < nc) *(u32x4*)((T*)a.y + r * a.y_st + k * VEC) = pack<T>(ys);
     }
-  }
+  };
+  if (fast)
+    norm_row(std::true_type{});
+  else
+    norm_row(std::false_type{});
 }
 
 struct SwigluArgs {
@@ -430,12 +439,13 @@ int32_t launch_wave_norm(const NormArgs& a, int nch, hipStream_t s) {
   const int64_t grid = (a.rows + kWaveNormRows - 1) / kWaveNormRows;
   if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "cev_rms_norm: too many rows");
   const dim3 g((unsigned)grid), b(kWaveNormRows * 64);
+  const bool res = a.h != nullptr;
   if (nch <= 4)
-    hipLaunchKernelGGL((rms_norm_wave_kernel<T, 4>), g, b, 0, s, a);
+    hipLaunchKernelGGL(res ? (rms_norm_wave_kernel<T, 4, true>) : (rms_norm_wave_kernel<T, 4, false>), g, b, 0, s, a);
   else if (nch <= 8)
-    hipLaunchKernelGGL((rms_norm_wave_kernel<T, 8>), g, b, 0, s, a);
+    hipLaunchKernelGGL(res ? (rms_norm_wave_kernel<T, 8, true>) : (rms_norm_wave_kernel<T, 8, false>), g, b, 0, s, a);
   else
-    hipLaunchKernelGGL((rms_norm_wave_kernel<T, 16>), g, b, 0, s, a);
+    hipLaunchKernelGGL(res ? (rms_norm_wave_kernel<T, 16, true>) : (rms_norm_wave_kernel<T, 16, false>), g, b, 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "cev_rms_norm launch: %s", hipGetErrorString(e));
   return CEV_OK;
