@@ -252,7 +252,7 @@ __device__ __forceinline__ uint64_t shfl_u64(uint64_t x, int src) {
 // Waves per SIMD the register budget is held to: the packed vector takes
 // D * sizeof(T) / 16 * 4 registers per lane.
 template <typename T, int D>
-constexpr int lane_waves() { return D * (int)sizeof(T) >= 512 ? 3 : 4; }
+constexpr int lane_waves() { return D * (int)sizeof(T) >= 512 ? 2 : 3; }
 
 template <typename T, int D, int ROT, int TPB>
 __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<T, D>()))) void qknorm_rope_lane_kernel(
@@ -264,9 +264,7 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<
   constexpr int HC = HALF / VEC;            // chunks in the first rotary half
   static_assert(HALF % VEC == 0 && ROT <= D, "rotary halves are whole chunks");
   auto rnd = [](float x) { return BF ? bf16_round(x) : x; };
-  // The weights as the norm multiplies them (1 + w rounded to the dtype
-  // for the zero-centred form), once per workgroup: q's then k's.
-  __shared__ __align__(16) float weff[2][D];
+  __shared__ __align__(16) float weff[2][D];  // the norm's weights, q's then k's
   // per wave: 64 vectors x 128 bytes (one staging round) + 16 bytes of pad
   constexpr int NR = NC / 8;  // staging rounds
   static_assert(NC % 8 == 0, "whole staging rounds");
@@ -275,20 +273,6 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<
     copy_v_rows<T, D>(a);
     return;
   }
-  for (int i = threadIdx.x; i < 2 * D; i += TPB) {
-    const T* wsrc = i < D ? (const T*)a.w_q : (const T*)a.w_k;
-    const bool have = i < D ? a.hq > 0 : a.hkv > 0;
-    float w = 0.0f;
-    if (have) {
-      if constexpr (BF)
-        w = bf16_from_bits(((const uint16_t*)wsrc)[i % D]);
-      else
-        w = ((const float*)wsrc)[i % D];
-      if (a.plus_one) w = rnd(w + 1.0f);
-    }
-    weff[i / D][i % D] = w;
-  }
-  __syncthreads();
 
   const int64_t nq = (int64_t)a.t * a.hq;
   const int64_t total = nq + (int64_t)a.t * a.hkv;
@@ -311,9 +295,13 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<
     tk = (int)(vk / a.hkv);
     const int h = (int)(vk % a.hkv);
     src = (const T*)a.k_in + tk * a.ki_st + h * a.ki_sh;
-    const int64_t r = kv_row(a, tk);
-    dst = r >= 0 ? (T*)a.k_out + r * a.ko_st + h * a.ko_sh : nullptr;
+    dst = (T*)a.k_out + h * a.ko_sh;  // the slot row is added below
   }
+  // Loads the epilogue needs go out before the staging loads, so that no
+  // dependent load waits behind them: the token's position and, for k, its
+  // cache slot (every lane reads one; q lanes ignore theirs).
+  const int p = a.pos[tk];
+  const int slot = a.slots ? a.slots[tk] : tk;
   const float* wl = weff[is_q ? 0 : 1];
   const int lane = threadIdx.x & 63;
   char* st = stage[threadIdx.x >> 6];
@@ -327,21 +315,63 @@ __global__ __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(lane_waves<
     gptr<const u32x4> vp[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) vp[i] = (gptr<const u32x4>)shfl_u64(sp, 8 * i + sub) + kc;
+    // The first two rounds' loads go out before the workgroup's weight
+    // loads, and each later round's two rounds ahead of its exchange (the LDS
+    // syncs fence memory operations), so the weights and a vector cost about
+    // one memory latency, not one per round.
+    u32x4 g0[8], g1[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) g0[i] = vp[i][0];
+    if (NR > 1) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) g1[i] = vp[i][8];
+    }
+    // The weights as the norm multiplies them (1 + w rounded to the dtype
+    // for the zero-centred form), once per workgroup: q's then k's.
+    // The loads are unconditional (a side with no heads reads the other
+    // side's weights and uses 0), so none waits behind a branch.
+    constexpr int WN = (2 * D + TPB - 1) / TPB;
+    const T* wsafe = a.hq > 0 ? (const T*)a.w_q : (const T*)a.w_k;
+    float wraw[WN];
+    bool whave[WN];
+#pragma unroll
+    for (int u = 0; u < WN; ++u) {
+      const int i = threadIdx.x + u * TPB;
+      whave[u] = i < 2 * D && (i < D ? a.hq > 0 : a.hkv > 0);
+      const T* wp = whave[u] ? (i < D ? (const T*)a.w_q : (const T*)a.w_k) + i % D : wsafe;
+      if constexpr (BF)
+        wraw[u] = bf16_from_bits(*(const uint16_t*)wp);
+      else
+        wraw[u] = *(const float*)wp;
+    }
+#pragma unroll
+    for (int u = 0; u < WN; ++u) {
+      const int i = threadIdx.x + u * TPB;
+      if (i < 2 * D) {
+        const float w = a.plus_one ? rnd(wraw[u] + 1.0f) : wraw[u];
+        weff[i / D][i % D] = whave[u] ? w : 0.0f;
+      }
+    }
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < NR; ++q) {
-      u32x4 g[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) g[i] = vp[i][8 * q];
+      u32x4* g = q % 2 == 0 ? g0 : g1;
 #pragma unroll
       for (int i = 0; i < 8; ++i) *(u32x4*)(st + (8 * i + sub) * kStageRow + 16 * kc) = g[i];
       wave_lds_sync();
 #pragma unroll
       for (int k = 0; k < 8; ++k) c[8 * q + k] = *(const u32x4*)(st + lane * kStageRow + 16 * k);
       wave_lds_sync();
+      if (q + 2 < NR) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) g[i] = vp[i][8 * (q + 2)];
+      }
     }
-
   }
-  const int p = a.pos[tk];
+  if (!is_q) {
+    const bool slot_ok = !a.slots || (slot >= 0 && slot < a.n_slots);
+    dst = slot_ok ? dst + (int64_t)slot * a.ko_st : nullptr;
+  }
 
   float sum2 = 0.0f;
   int min_exp = 0;  // smallest frexp exponent of a nonzero element (0 for 0)
