@@ -563,21 +563,6 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
     copy_v_rows<T, D>(a);
     return;
   }
-  for (int i = threadIdx.x; i < 2 * D; i += kQuadThreads) {
-    const T* wsrc = i < D ? (const T*)a.w_q : (const T*)a.w_k;
-    const bool have = i < D ? a.hq > 0 : a.hkv > 0;
-    float w = 0.0f;
-    if (have) {
-      if constexpr (BF)
-        w = bf16_from_bits(((const uint16_t*)wsrc)[i % D]);
-      else
-        w = ((const float*)wsrc)[i % D];
-      if (a.plus_one) w = rnd(w + 1.0f);
-    }
-    weff[i / D][i % D] = w;
-  }
-  __syncthreads();
-
   const int64_t nq = (int64_t)a.t * a.hq;
   const int64_t total = nq + (int64_t)a.t * a.hkv;
   const int j = threadIdx.x & 3;
@@ -600,14 +585,56 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
     tk = (int)(vk / a.hkv);
     const int h = (int)(vk % a.hkv);
     src = (const T*)a.k_in + tk * a.ki_st + h * a.ki_sh;
-    const int64_t r = kv_row(a, tk);
-    dst = r >= 0 ? (T*)a.k_out + r * a.ko_st + h * a.ko_sh : nullptr;
+    dst = (T*)a.k_out + h * a.ko_sh;  // the slot row is added below
   }
-  const float* wl = weff[is_q ? 0 : 1] + j * E;
+  // Every load the lane needs goes out before the first wait: its quarter of
+  // the vector, the token's position and cache slot (q lanes ignore theirs)
+  // and the workgroup's weights.  The weight loads are unconditional (a side
+  // with no heads reads the other side's weights and stores 0), so none
+  // waits behind a branch.
   u32x4 c[NCL];
 #pragma unroll
   for (int k = 0; k < NCL; ++k) c[k] = *(const u32x4*)(src + j * E + k * VEC);
   const int p = a.pos[tk];
+  const int slot = a.slots ? a.slots[tk] : tk;
+  constexpr int WN = 2 * D / kQuadThreads;
+  static_assert(2 * D % kQuadThreads == 0, "whole weight rounds");
+  const T* wsafe = a.hq > 0 ? (const T*)a.w_q : (const T*)a.w_k;
+  float wraw[WN];
+#pragma unroll
+  for (int u = 0; u < WN; ++u) {
+    const int i = threadIdx.x + u * kQuadThreads;
+    const bool have = i < D ? a.hq > 0 : a.hkv > 0;
+    const T* wp = have ? (i < D ? (const T*)a.w_q : (const T*)a.w_k) + i % D : wsafe;
+    if constexpr (BF)
+      wraw[u] = bf16_from_bits(*(const uint16_t*)wp);
+    else
+      wraw[u] = *(const float*)wp;
+    wraw[u] = have ? (a.plus_one ? rnd(wraw[u] + 1.0f) : wraw[u]) : 0.0f;
+  }
+  // the rotation's cos/sin chunks, loaded as soon as the position is known
+  const bool p_ok = p >= 0 && p < a.n_pos;
+  const T* crow = (const T*)a.cos_t + (int64_t)(p_ok ? p : 0) * (ROT / 2);
+  const T* srow = (const T*)a.sin_t + (int64_t)(p_ok ? p : 0) * (ROT / 2);
+  constexpr int NT = ROT == D ? NCL : NCL / 2;  // table chunks a lane reads
+  const int tb = ROT == D ? (j & 1) * E : 0;     // table index of its first element
+  u32x4 ctab[NT], stab[NT];
+#pragma unroll
+  for (int k = 0; k < NT; ++k) {
+    ctab[k] = *(const u32x4*)(crow + tb + k * VEC);
+    stab[k] = *(const u32x4*)(srow + tb + k * VEC);
+  }
+#pragma unroll
+  for (int u = 0; u < WN; ++u) {
+    const int i = threadIdx.x + u * kQuadThreads;
+    weff[i / D][i % D] = wraw[u];
+  }
+  __syncthreads();
+  if (!is_q) {
+    const bool slot_ok = !a.slots || (slot >= 0 && slot < a.n_slots);
+    dst = slot_ok ? dst + (int64_t)slot * a.ko_st : nullptr;
+  }
+  const float* wl = weff[is_q ? 0 : 1] + j * E;
 
   // smallest frexp exponent of a nonzero element over the quad (0 for 0)
   int min_exp = 0;
@@ -638,9 +665,6 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
   const float m = rnd(sqrtf(sum2 / (float)D + a.eps));
   const bool fast = min_exp >= -95 && sum2 <= 0x1p120f && m >= 0x1p-20f && m <= 0x1p20f;
   const float y = 1.0f / m;
-  const bool p_ok = p >= 0 && p < a.n_pos;
-  const T* crow = (const T*)a.cos_t + (int64_t)(p_ok ? p : 0) * (ROT / 2);
-  const T* srow = (const T*)a.sin_t + (int64_t)(p_ok ? p : 0) * (ROT / 2);
 
   auto body = [&](auto fast_c) {
     constexpr bool FAST = decltype(fast_c)::value;
@@ -662,7 +686,6 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
       //   x_i'         = dtype(x_i c) - dtype(x_{i+D/2} s)   (j < 2),
       //   x_{i+D/2}'   = dtype(x_i s) + dtype(x_{i+D/2} c)   (j >= 2).
       const bool first = j < 2;
-      const int ib = (j & 1) * E;  // table index of this lane's first element
 #pragma unroll
       for (int k = 0; k < NCL; ++k) {
         float yo[VEC], yp[VEC];
@@ -670,7 +693,7 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
         for (int e = 0; e < VEC; ++e) yo[e] = norm(c[k], k, e);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) yp[e] = dpp_f<0x4E>(yo[e]);  // the partner's (lane ^ 2)
-        const u32x4 cc = *(const u32x4*)(crow + ib + k * VEC), sc = *(const u32x4*)(srow + ib + k * VEC);
+        const u32x4 cc = ctab[k], sc = stab[k];
         float r[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
@@ -690,7 +713,7 @@ __global__ __launch_bounds__(kQuadThreads) void qknorm_rope_quad_kernel(QkArgs a
       if (j == 0) {
 #pragma unroll
         for (int k = 0; k < HC; ++k) {
-          const u32x4 cc = *(const u32x4*)(crow + k * VEC), sc = *(const u32x4*)(srow + k * VEC);
+          const u32x4 cc = ctab[k], sc = stab[k];
           float r0[VEC], r1[VEC];
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
