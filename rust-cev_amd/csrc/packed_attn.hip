@@ -57,10 +57,17 @@ constexpr float kRescale = 8.0f;
 // host plan is never followed: the attention kernels fill the whole output
 // with NaN instead (poison_output) and the merge pass writes nothing, so a
 // stale device plan shows in the result rather than leaving rows unwritten.
-__device__ __forceinline__ bool plan_ok(const AttnArgs& a) {
-  const cev_plan_header* h = (const cev_plan_header*)a.plan;
-  return h->magic == CEV_PLAN_MAGIC && (uint32_t)h->sig == a.plan_sig && h->n_tiles == a.n_tiles && h->t == a.t &&
-         h->s_cache == a.s_cache && h->n_splits == a.n_splits;
+// The header is read at once and every field compared (no short-circuit,
+// which would make each field a dependent load).
+// The header stays in h for the offsets the kernel reads next.
+__device__ __forceinline__ bool plan_ok(const AttnArgs& a, cev_plan_header& h) {
+  h = *(const cev_plan_header*)a.plan;
+  // the section offsets follow the header in order (this also loads them
+  // with the other fields)
+  constexpr int32_t kHeaderWords = (int32_t)(sizeof(cev_plan_header) / 4);
+  return (h.magic == CEV_PLAN_MAGIC) & ((uint32_t)h.sig == a.plan_sig) & (h.n_tiles == a.n_tiles) & (h.t == a.t) &
+         (h.s_cache == a.s_cache) & (h.n_splits == a.n_splits) & (h.tiles_off >= kHeaderWords) & (h.segs_off >= h.tiles_off) &
+         (h.rows_off >= h.segs_off);
 }
 
 // Workgroup b of the grid writes NaN over output rows [b t / G, (b+1) t / G)
@@ -549,7 +556,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   using namespace pipe;
   __shared__ __align__(16) char lds[2 * kBuf * kTileBytes];
 
-  if (!plan_ok(a)) {
+  cev_plan_header ph;
+  if (!plan_ok(a, ph)) {
     poison_output<T, D>(a);
     return;
   }
@@ -558,12 +566,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   const int kvh = blockIdx.x % a.hkv;
   const int item = blockIdx.x / a.hkv;
   const int tile = item / a.n_splits, part = item % a.n_splits;
-  const cev_plan_header* ph = (const cev_plan_header*)a.plan;
-  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[2 * tile];
-  const int n_chunks = ((const int4*)(a.plan + ph->tiles_off))[2 * tile + 1].x;
-  const int4* segs = (const int4*)(a.plan + ph->segs_off) + td.z;
+  const int4* tdp = (const int4*)(a.plan + ph.tiles_off) + 2 * tile;
+  const int4 td = tdp[0];
+  const int n_chunks = tdp[1].x;
+  const int4* segs = (const int4*)(a.plan + ph.segs_off) + td.z;
   const int nseg = td.w;
-  const int4* rows = (const int4*)(a.plan + ph->rows_off);
+  const int4* rows = (const int4*)(a.plan + ph.rows_off);
   // Query slot (wave, n) holds row slot / g of the tile, query head slot % g:
   // the valid rows of a short tile fill the first waves, and a wave with no
   // valid row skips the MFMA work (it still fetches its share of K/V).
@@ -903,7 +911,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
   using P = typename F::P;
   __shared__ __align__(16) T smem[2 * TILE];
 
-  if (!plan_ok(a)) {
+  cev_plan_header ph;
+  if (!plan_ok(a, ph)) {
     poison_output<T, D>(a);
     return;
   }
@@ -912,12 +921,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
   const int kvh = blockIdx.x % a.hkv;
   const int item = blockIdx.x / a.hkv;
   const int tile = item / a.n_splits, part = item % a.n_splits;
-  const cev_plan_header* ph = (const cev_plan_header*)a.plan;
-  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[2 * tile];
-  const int n_chunks = ((const int4*)(a.plan + ph->tiles_off))[2 * tile + 1].x;
-  const int4* segs = (const int4*)(a.plan + ph->segs_off) + td.z;
+  const int4* tdp = (const int4*)(a.plan + ph.tiles_off) + 2 * tile;
+  const int4 td = tdp[0];
+  const int n_chunks = tdp[1].x;
+  const int4* segs = (const int4*)(a.plan + ph.segs_off) + td.z;
   const int nseg = td.w;
-  const int4* rows = (const int4*)(a.plan + ph->rows_off);
+  const int4* rows = (const int4*)(a.plan + ph.rows_off);
   // Query slot (wave, n) holds row slot / g of the tile, query head slot % g:
   // the valid rows of a short tile fill the first waves, and a wave with no
   // valid row skips the MFMA work (it still helps stage K/V).
@@ -1154,7 +1163,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
   constexpr int NDT = D / 32;
   __shared__ __align__(16) char lds[2 * kBuf * kTileBytes];
 
-  if (!plan_ok(a)) {
+  cev_plan_header ph;
+  if (!plan_ok(a, ph)) {
     poison_output<T, D>(a);
     return;
   }
@@ -1163,12 +1173,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
   const int kvh = blockIdx.x % a.hkv;
   const int item = blockIdx.x / a.hkv;
   const int tile = item / a.n_splits, part = item % a.n_splits;
-  const cev_plan_header* ph = (const cev_plan_header*)a.plan;
-  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[2 * tile];
-  const int n_chunks = ((const int4*)(a.plan + ph->tiles_off))[2 * tile + 1].x;
-  const int4* segs = (const int4*)(a.plan + ph->segs_off) + td.z;
+  const int4* tdp = (const int4*)(a.plan + ph.tiles_off) + 2 * tile;
+  const int4 td = tdp[0];
+  const int n_chunks = tdp[1].x;
+  const int4* segs = (const int4*)(a.plan + ph.segs_off) + td.z;
   const int nseg = td.w;
-  const int4* rows = (const int4*)(a.plan + ph->rows_off);
+  const int4* rows = (const int4*)(a.plan + ph.rows_off);
   // Query slot (wave, n) holds row slot / g of the tile, query head slot % g;
   // a wave with no valid row skips the MFMA work and still fetches its rows.
   const int slot = wave * 32 + n;
@@ -1422,23 +1432,29 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
   constexpr int Q = D / 4;    // 4-column groups of a record
   constexpr int PS = 64 / Q;  // parts read side by side: 2 at d = 128, 1 at d = 256
   static_assert(Q * PS == 64, "one wave covers the head dim");
-  if (!plan_ok(a)) return;
-  const cev_plan_header* ph = (const cev_plan_header*)a.plan;
+  cev_plan_header ph;
+  if (!plan_ok(a, ph)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // blockIdx -> (tile, row group of kMergeWaves rows, head)
-  const int tile_rows = ph->tile_rows;
+  const int tile_rows = a.tile_rows;  // validated against the plan at launch
   const int groups = (tile_rows + kMergeWaves - 1) / kMergeWaves;
   const int head = blockIdx.x % a.hq;
   const int grp = (blockIdx.x / a.hq) % groups;
   const int tile = blockIdx.x / (a.hq * groups);
-  const int4 td = ((const int4*)(a.plan + ph->tiles_off))[2 * tile];
+  const int4 td = ((const int4*)(a.plan + ph.tiles_off))[2 * tile];
   const int r = grp * kMergeWaves + wave;
-  if (r >= td.y || td.x + r >= a.t) return;
+  if ((r >= td.y) | (td.x + r >= a.t)) return;
   const int row = td.x + r;
   const int64_t pf = cev_attn_partial_floats(D);
   const int S = a.n_splits;
   const int col = lane % Q, phase = lane / Q;
   const float* rec = a.ws + ((int64_t)row * a.hq + head) * S * pf;
+  // The gate chunk loads with the first records (from a record when there
+  // is no gate, and is then unused), not after the merge.
+  const int d = 4 * col;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh + d : (const T*)rec;
+  float gv[4];
+  load_vec4<T>(gp, gv);
 
   // Every record holds a finite m (a part with no visible key keeps its
   // initial -1e30 and l = 0), so M is finite after the first batch.
@@ -1481,15 +1497,12 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
     if (phase != 0) return;
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  const int d = 4 * col;
   T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh + d;
-  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh + d : nullptr;
-  float v[4], gv[4];
-  if (gp) load_vec4<T>(gp, gv);
+  float v[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     float x = BF ? acc[e] * inv : (L > 0.0f ? acc[e] / L : 0.0f);
-    if (gp) x = gate_value(x, gv[e], BF);
+    if (a.has_gate) x = gate_value(x, gv[e], BF);
     v[e] = x;
   }
   store_vec4<T>(op, v);
