@@ -22,6 +22,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 
 #include "cev_device.h"
 #include "cev_internal.h"
@@ -70,8 +71,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 // One wave per output column j: the lanes stream w's row j in 16-byte
 // chunks (read once), multiply it with each of the m <= MR input rows (hot
 // in L2) and reduce across the wave.  f32 accumulation; k a multiple of the
-// 16-byte chunk (checked by the launcher).
-template <typename T, typename TO, int MR>
+// 16-byte chunk (checked by the launcher).  A lane's chunks are loaded NB at
+// a time with clamped indices (rows past m read row m - 1, chunks past k the
+// last chunk), so every load of a batch is unconditional and in flight
+// together; only the accumulation skips them.  Each lane still adds its
+// chunks in order.
+template <typename T, typename TO, int MR, int NB>
 __global__ __launch_bounds__(kLinWaves * 64) void linear_rows_kernel(LinArgs a) {
   constexpr int VEC = 16 / (int)sizeof(T);
   const int lane = threadIdx.x & 63;
@@ -81,25 +86,32 @@ __global__ __launch_bounds__(kLinWaves * 64) void linear_rows_kernel(LinArgs a) 
   float acc[MR];
 #pragma unroll
   for (int r = 0; r < MR; ++r) acc[r] = 0.0f;
-  for (int64_t e = (int64_t)lane * VEC; e < a.k; e += 64 * VEC) {
-    T wv[VEC];
-    *(uint4*)wv = *(const uint4*)(wr + e);
+  for (int64_t e0 = (int64_t)lane * VEC; e0 < a.k; e0 += (int64_t)NB * 64 * VEC) {
+    uint4 wv[NB], xv[MR][NB];
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-      if (r < a.m) {
-        T xv[VEC];
-        *(uint4*)xv = *(const uint4*)((const T*)a.x + r * a.ldx + e);
+    for (int b = 0; b < NB; ++b) {
+      const int64_t ec = min(e0 + (int64_t)b * 64 * VEC, a.k - VEC);
+      wv[b] = *(const uint4*)(wr + ec);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[r] = __builtin_fmaf(to_f32<T>(xv[i]), to_f32<T>(wv[i]), acc[r]);
+      for (int r = 0; r < MR; ++r) xv[r][b] = *(const uint4*)((const T*)a.x + (int64_t)min(r, (int)a.m - 1) * a.ldx + ec);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (e0 + (int64_t)b * 64 * VEC < a.k) {
+        const T* w8 = (const T*)&wv[b];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          const T* x8 = (const T*)&xv[r][b];
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[r] = __builtin_fmaf(to_f32<T>(x8[i]), to_f32<T>(w8[i]), acc[r]);
+        }
       }
     }
   }
 #pragma unroll
   for (int r = 0; r < MR; ++r) {
-    if (r < a.m) {
-      const float s = wave_sum(acc[r]);
-      if (lane == 0) ((TO*)a.y)[r * a.ldy + j] = from_f32<TO>(s * a.alpha);
-    }
+    const float s = wave_sum(acc[r]);
+    if (r < a.m && lane == 0) ((TO*)a.y)[r * a.ldy + j] = from_f32<TO>(s * a.alpha);
   }
 }
 
@@ -201,10 +213,23 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 template <typename T>
 int32_t launch_rows(const LinArgs& a, int out_dtype, hipStream_t s) {
   const dim3 grid((unsigned)((a.n + kLinWaves - 1) / kLinWaves)), block(kLinWaves * 64);
-  if (out_dtype == CEV_F32)
-    hipLaunchKernelGGL((linear_rows_kernel<T, float, kRowsSmall>), grid, block, 0, s, a);
+  // rows held per lane and chunks loaded per batch: fewer rows, deeper batches
+  auto go = [&](auto mr_c, auto nb_c) {
+    constexpr int MR = decltype(mr_c)::value, NB = decltype(nb_c)::value;
+    if (out_dtype == CEV_F32)
+      hipLaunchKernelGGL((linear_rows_kernel<T, float, MR, NB>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((linear_rows_kernel<T, T, MR, NB>), grid, block, 0, s, a);
+  };
+  using std::integral_constant;
+  if (a.m <= 1)
+    go(integral_constant<int, 1>{}, integral_constant<int, 8>{});
+  else if (a.m <= 2)
+    go(integral_constant<int, 2>{}, integral_constant<int, 8>{});
+  else if (a.m <= 4)
+    go(integral_constant<int, 4>{}, integral_constant<int, 4>{});
   else
-    hipLaunchKernelGGL((linear_rows_kernel<T, T, kRowsSmall>), grid, block, 0, s, a);
+    go(integral_constant<int, kRowsSmall>{}, integral_constant<int, 4>{});
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "cev_linear launch: %s", hipGetErrorString(e));
   return CEV_OK;
