@@ -1088,10 +1088,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
 // bf16, d = 256: the sequential chunk body of attn_kernel_seq (score, softmax,
 // then multiply into O) fed the way attn_kernel_pipe is fed.  32-key chunks
 // go from HBM straight into a ring of kBuf LDS buffers (buffer_load ... lds),
-// kAhead chunks in flight ahead of the one being scored, so no register
-// holds staged K/V and a chunk's fetch latency is spread over three chunk
-// bodies instead of one.  Rows are 512 bytes, unpadded, with the 16-byte
-// column blocks permuted for conflict-free operand reads:
+// fetched kAhead chunks ahead of the one being scored, so no register holds
+// staged K/V and a chunk has two chunk bodies to land (the body before its
+// own reads its first K fragments) instead of none.  Rows are 512 bytes,
+// unpadded, with the 16-byte column blocks permuted for conflict-free
+// operand reads:
 //   K: block c of row r at slot c ^ (r & 15)     (ds_read_b128, one key row
 //      per lane: 16 rows cover every bank once)
 //   V: block c of row r at slot c ^ 4(r & 3)     (ds_read_b64_tr_b16, four
