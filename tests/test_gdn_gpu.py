@@ -114,6 +114,30 @@ def test_gdn_carried_state_vs_oracle(gpu, orc, bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("kernel", [2, 3, 5, 7, 8])
+def test_gdn_conv_widths_vs_oracle(gpu, orc, bf16, kernel):
+    """Every conv width the library builds a kernel for besides 4 (widths 7
+    and 8 run 512-thread workgroups), with a carried conv state and a
+    sequence that ends inside a chunk and inside a conv run."""
+    w = configs.GdnWorkload("gdn-width", 13, bf16, 2, 133, nk=2, nv=4, kernel=kernel)
+    _say(f"test gdn conv width {kernel}: bf16={bf16} T={w.t}")
+    inp = w.inputs()
+    rng = np.random.default_rng(4 + kernel)
+    conv_in = rng.standard_normal((w.batch, w.conv_dim, kernel - 1)).astype(np.float32)
+    if bf16:
+        conv_in = cev_hip.synth.round_bf16(conv_in)
+    y, co, so = _run_gpu(w, inp, gpu, conv_in=to_dev(conv_in, bf16, gpu))
+    ry, rco, rso = _run_oracle(orc, w, inp, conv_in=conv_in)
+    ey = float(np.abs(to_np(y) - ry).max())
+    es = float(np.abs(to_np(so) - rso).max())
+    _say(f"  max|d| y {ey:.3g}  state {es:.3g}")
+    assert to_np(co).shape == (w.batch, w.conv_dim, kernel - 1)
+    assert np.array_equal(to_np(co), rco)
+    assert es <= F32_TOL
+    assert ey <= (BF16_TOL if bf16 else F32_TOL)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
 def test_gdn_strided_views_vs_oracle(gpu, orc, bf16):
     """z as a column slice of a wider tensor (odd row stride, a view into a
     fused projection output) and y written into such a view: the
