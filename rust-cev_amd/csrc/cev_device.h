@@ -46,6 +46,39 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The bf16 SiLU of a bf16 value, v / (1 + e^-v) with each op rounded to
+// bf16, depends on its 16 bits only.  Kernels that apply it to many values
+// tabulate it in LDS for |v| in [2^-16, 2^7) (23 binades of 128 mantissas
+// per sign), evaluated by the same silu_bf16, so a table hit is
+// bit-identical to evaluating it; values outside take silu_bf16 itself.
+// (The translation units that use it are built without FMA contraction.)
+constexpr uint32_t kSiluLo = (127 - 16) * 128;  // |bits| of 2^-16
+constexpr uint32_t kSiluSpan = 23 * 128;        // entries per sign
+constexpr int kSiluEntries = 2 * (int)kSiluSpan;
+
+__device__ __forceinline__ float silu_bf16(float v) {
+  const float ex = bf16_round(expf(-v));
+  const float den = bf16_round(1.0f + ex);
+  return bf16_round(v / den);
+}
+
+// table slot of a bf16-exact value: negative values after the positive ones;
+// >= kSiluEntries when |v| is outside the table
+__device__ __forceinline__ uint32_t silu_slot(float v) {
+  const uint32_t b = __float_as_uint(v) >> 16;
+  const uint32_t m = (b & 0x7fffu) - kSiluLo;
+  return m < kSiluSpan ? m + (b >> 15) * kSiluSpan : (uint32_t)kSiluEntries;
+}
+
+// Every thread of a workgroup of `threads` fills its share of the table.
+__device__ __forceinline__ void silu_fill(float* tab, int threads) {
+  for (int i = threadIdx.x; i < kSiluEntries; i += threads) {
+    const uint32_t neg = i >= (int)kSiluSpan;
+    const uint32_t bits = (neg << 15) | (kSiluLo + (uint32_t)i - neg * kSiluSpan);
+    tab[i] = silu_bf16(bf16_from_bits((uint16_t)bits));
+  }
+}
+
 template <typename Fn, int... I>
 __device__ __forceinline__ void static_for_impl(Fn&& f, std::integer_sequence<int, I...>) {
   (f(std::integral_constant<int, I>{}), ...);

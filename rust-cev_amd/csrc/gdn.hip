@@ -128,28 +128,9 @@ constexpr int kConvCus = 256;
 // 128 registers that leaves each lane, so they run 8 waves
 constexpr int conv_threads(int K) { return K <= 6 ? 1024 : 512; }
 
-// The bf16 SiLU of a bf16 value depends on its 16 bits only.  Each conv
-// workgroup first tabulates it in LDS for |v| in [2^-16, 2^7) (23 binades of
-// 128 mantissas per sign), evaluated by the same silu_bf16 below, so a table
-// hit is bit-identical to evaluating it.  A token whose 8 x 64 values are not
-// all in that range takes silu_bf16 itself (wave-uniform branch).
-constexpr uint32_t kSiluLo = (127 - 16) * 128;  // |bits| of 2^-16
-constexpr uint32_t kSiluSpan = 23 * 128;        // entries per sign
-constexpr int kSiluEntries = 2 * (int)kSiluSpan;
-
-__device__ __forceinline__ float silu_bf16(float v) {
-  const float ex = bf16_round(expf(-v));
-  const float den = bf16_round(1.0f + ex);
-  return bf16_round(v / den);
-}
-
-// table slot of a bf16-exact value: negative values after the positive ones;
-// >= kSiluEntries when |v| is outside the table
-__device__ __forceinline__ uint32_t silu_slot(float v) {
-  const uint32_t b = __float_as_uint(v) >> 16;
-  const uint32_t m = (b & 0x7fffu) - kSiluLo;
-  return m < kSiluSpan ? m + (b >> 15) * kSiluSpan : (uint32_t)kSiluEntries;
-}
+// Each conv workgroup first tabulates the bf16 SiLU in LDS (silu_fill), and
+// a token whose 8 x 64 values are not all in the table's range takes
+// silu_bf16 itself (wave-uniform branch).
 
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
@@ -304,11 +285,7 @@ __global__ __launch_bounds__(conv_threads(K)) void gdn_conv_kernel(GdnArgs g) {
   constexpr int kConvThreads = conv_threads(K);
   __shared__ float silu_tab[sizeof(T) == 2 ? kSiluEntries : 1];
   if constexpr (sizeof(T) == 2) {
-    for (int i = threadIdx.x; i < kSiluEntries; i += kConvThreads) {
-      const uint32_t neg = i >= (int)kSiluSpan;
-      const uint32_t bits = (neg << 15) | (kSiluLo + (uint32_t)i - neg * kSiluSpan);
-      silu_tab[i] = silu_bf16(bf16_from_bits((uint16_t)bits));
-    }
+    silu_fill(silu_tab, kConvThreads);
     __syncthreads();
   }
   const int64_t cg = g.conv_dim / 8;

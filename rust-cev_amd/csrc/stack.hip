@@ -321,6 +321,58 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// bf16 with the SiLU table: up to kSwigluBlocks workgroups, each filling
+// the table once and then taking rows blockIdx.x, blockIdx.x + gridDim.x, ...;
+// a thread loads kSwigluAhead chunks of g and u of a row (indices clamped to
+// the row, so the loads are unconditional) before computing them.  A chunk
+// slot whose gate values are not all in the table takes silu_bf16 for the
+// whole wave.  Bit-identical to swiglu_kernel<bf16>.
+constexpr int kSwigluThreads = 256;
+constexpr int kSwigluAhead = 4;
+constexpr int kSwigluBlocks = 1024;  // four workgroups per CU, 23 KB of table each
+__global__ __launch_bounds__(kSwigluThreads) void swiglu_table_kernel(SwigluArgs a) {
+  constexpr int VEC = 8;
+  __shared__ float silu_tab[kSiluEntries];
+  silu_fill(silu_tab, kSwigluThreads);
+  __syncthreads();
+  const int nc = a.inter / VEC;
+  for (int64_t r = blockIdx.x; r < a.rows; r += gridDim.x) {
+    const uint16_t* gr = (const uint16_t*)a.g + r * a.in_st;
+    const uint16_t* ur = (const uint16_t*)a.u + r * a.in_st;
+    uint16_t* orow = (uint16_t*)a.out + r * a.out_st;
+    for (int k0 = threadIdx.x; k0 < nc; k0 += kSwigluThreads * kSwigluAhead) {
+      u32x4 cg[kSwigluAhead], cu[kSwigluAhead];
+#pragma unroll
+      for (int u = 0; u < kSwigluAhead; ++u) {
+        const int k = min(k0 + u * kSwigluThreads, nc - 1);
+        cg[u] = *(const u32x4*)(gr + k * VEC);
+        cu[u] = *(const u32x4*)(ur + k * VEC);
+      }
+#pragma unroll
+      for (int u = 0; u < kSwigluAhead; ++u) {
+        const int k = k0 + u * kSwigluThreads;
+        uint32_t slot[VEC];
+        bool hit = true;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          slot[j] = silu_slot(elem<uint16_t>(cg[u], j));
+          hit = hit && slot[j] < (uint32_t)kSiluEntries;
+        }
+        float o[VEC];
+        if (__all(hit)) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) o[j] = bf16_round(silu_tab[slot[j]] * elem<uint16_t>(cu[u], j));
+        } else {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) o[j] = bf16_round(silu_bf16(elem<uint16_t>(cg[u], j)) * elem<uint16_t>(cu[u], j));
+        }
+        if (k < nc) *(u32x4*)(orow + k * VEC) = pack<uint16_t>(o);
+      }
+    }
+  }
+}
+
+
 
 // ---------------------------------------------------------------------------
 // Debiased readout scores (Service::run_debiased's averaging,
@@ -491,7 +543,7 @@ extern "C" int32_t cev_swiglu(int32_t dtype, int64_t rows, int32_t inter, const 
   if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "cev_swiglu: too many rows");
   hipStream_t s = (hipStream_t)stream;
   if (dtype == CEV_BF16)
-    hipLaunchKernelGGL(swiglu_kernel<uint16_t>, dim3((unsigned)grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(swiglu_table_kernel, dim3((unsigned)std::min<int64_t>(rows, kSwigluBlocks)), dim3(kSwigluThreads), 0, s, a);
   else
     hipLaunchKernelGGL(swiglu_kernel<float>, dim3((unsigned)grid), dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
