@@ -33,7 +33,7 @@ PEAK_HBM_GBPS = 8000.0
 
 
 def traffic_from_profiles(workload: str):
-    """HBM bytes per K2 launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    """HBM bytes per K2 launch (or per GDN forward call) measured with rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by a copy-kernel calibration), if recorded."""
     path = os.path.join(ROOT, "profiles", "packed_attn_traffic.md")
     if not os.path.exists(path):
@@ -195,7 +195,7 @@ def calibrate_gemm(n: int, steps: int, warmup: int):
     print(json.dumps(out), flush=True)
 
 
-def bench_gdn(args, w, dev):
+def bench_gdn(args, w, dev, traffic_key: str):
     """One step = the GatedDeltaNet layer core (four kernels) over the batch."""
     import numpy as np
     import torch
@@ -256,7 +256,8 @@ def bench_gdn(args, w, dev):
                                f"dk={w.dk} dv={w.dv}, conv kernel {w.kernel}, 64-token chunks, "
                                f"{'bf16' if w.bf16 else 'f32'} inputs, f32 chunk rule",
                    "launch": "hip graph replay" if args.graph else "direct launches"},
-        "roofline": roofline(w.flops(), alg, layer_ms, "f32", "gdn conv + prep + scan + norm (one forward call)", None),
+        "roofline": roofline(w.flops(), alg, layer_ms, "f32", "gdn conv + prep + scan + norm (one forward call)",
+                             traffic_from_profiles(traffic_key)),
         "device": device_info().name,
     }
     if args.cpu_baseline:
@@ -452,13 +453,13 @@ def main():
         calibrate_gemm(args.calibrate_gemm, args.steps, args.warmup)
         return
     if args.workload == "c5gdn":
-        bench_gdn(args, configs.c5_gdn(), dev)
+        bench_gdn(args, configs.c5_gdn(), dev, "c5gdn")
         return
     if args.workload == "c2":
         bench_stack(args, configs.c2(True), dev)
         return
     if args.workload == "c5gdnrows":
-        bench_gdn(args, configs.GdnWorkload("c5gdn32x64", 5, True, 32, 64), dev)
+        bench_gdn(args, configs.GdnWorkload("c5gdn32x64", 5, True, 32, 64), dev, "c5gdnrows")
         return
     if args.calibrate_copy:
         n = args.calibrate_copy << 20
