@@ -1168,34 +1168,50 @@ __global__ __launch_bounds__(256) void gdn_norm_kernel(GdnArgs g) {
 }
 
 // The same with 16 lanes per (row, token, value head), 8 elements each:
-// 16-byte loads and stores, the sum of squares over the row by DPP.  Needs
-// z and y rows 16-byte aligned (checked by the launcher).
+// 16-byte loads and stores, the sum of squares over the row by DPP.  Each
+// 16-lane group takes kNormRows rows, 16 rows apart so that every load
+// instruction of the workgroup covers 16 consecutive rows, and issues all
+// their core and z loads before the first sum.  Needs z and y rows 16-byte
+// aligned (checked by the launcher).
+constexpr int kNormRows = 2;
+
 template <typename T>
 __global__ __launch_bounds__(256) void gdn_norm_vec_kernel(GdnArgs g) {
   const int sub = threadIdx.x & 15;
   const int64_t n_items = (int64_t)g.batch * g.t * g.nv;
-  const int64_t item = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  // rows past the end recompute the last row (the DPP sum needs all 16
-  // lanes of a row) and store nothing
-  const int64_t it = item < n_items ? item : n_items - 1;
-  const int h = (int)(it % g.nv);
-  const int64_t rt = it / g.nv;
-  const int t = (int)(rt % g.t), r = (int)(rt / g.t);
-  const float* cp = g.core + it * kD + 8 * sub;
-  const f32x4 c0 = *(const f32x4*)cp, c1 = *(const f32x4*)(cp + 4);
-  const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-  float zv[8];
-  load8<T>((const T*)g.z + r * g.z_sb + (int64_t)t * g.z_st + h * kD + 8 * sub, zv);
+  const int64_t first = (int64_t)blockIdx.x * (16 * kNormRows) + (threadIdx.x >> 4);
+  f32x4 c0[kNormRows], c1[kNormRows];
+  float zv[kNormRows][8];
+  int64_t yoff[kNormRows];
+#pragma unroll
+  for (int k = 0; k < kNormRows; ++k) {
+    // rows past the end recompute the last row (the DPP sum needs all 16
+    // lanes of a row) and store nothing
+    const int64_t item = first + 16 * k;
+    const int64_t it = item < n_items ? item : n_items - 1;
+    const int h = (int)(it % g.nv);
+    const int64_t rt = it / g.nv;
+    const int t = (int)(rt % g.t), r = (int)(rt / g.t);
+    const float* cp = g.core + it * kD + 8 * sub;
+    c0[k] = *(const f32x4*)cp;
+    c1[k] = *(const f32x4*)(cp + 4);
+    load8<T>((const T*)g.z + r * g.z_sb + (int64_t)t * g.z_st + h * kD + 8 * sub, zv[k]);
+    yoff[k] = r * g.y_sb + (int64_t)t * g.y_st + h * kD + 8 * sub;
+  }
   const f32x4 w0 = *(const f32x4*)(g.norm_w + 8 * sub), w1 = *(const f32x4*)(g.norm_w + 8 * sub + 4);
   const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-  float s = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s += cv[e] * cv[e];
-  const float inv = 1.0f / sqrtf(row16_sum(s) / (float)kD + g.eps);
-  float y[8];
+  for (int k = 0; k < kNormRows; ++k) {
+    const float cv[8] = {c0[k][0], c0[k][1], c0[k][2], c0[k][3], c1[k][0], c1[k][1], c1[k][2], c1[k][3]};
+    float s = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = gated_norm(cv[e], inv, wv[e], zv[e]);
-  if (item < n_items) store8<T>((T*)g.y + r * g.y_sb + (int64_t)t * g.y_st + h * kD + 8 * sub, y);
+    for (int e = 0; e < 8; ++e) s += cv[e] * cv[e];
+    const float inv = 1.0f / sqrtf(row16_sum(s) / (float)kD + g.eps);
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = gated_norm(cv[e], inv, wv[e], zv[k][e]);
+    if (first + 16 * k < n_items) store8<T>((T*)g.y + yoff[k], y);
+  }
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1360,7 +1376,7 @@ extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, con
   const bool norm_vec = ((uintptr_t)g.z | (uintptr_t)g.y | (uintptr_t)g.norm_w) % 16 == 0 && g.z_sb % vec == 0 && g.z_st % vec == 0 &&
                         g.y_sb % vec == 0 && g.y_st % vec == 0;
   if (norm_vec) {
-    const dim3 grid((unsigned)((norm_items + 15) / 16));
+    const dim3 grid((unsigned)((norm_items + 16 * kNormRows - 1) / (16 * kNormRows)));
     if (d->dtype == CEV_BF16)
       hipLaunchKernelGGL(gdn_norm_vec_kernel<__bf16>, grid, dim3(256), 0, s, g);
     else
