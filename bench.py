@@ -171,6 +171,31 @@ def capture(fns):
     return graphs
 
 
+SETTLE = {"ms": 0.0, "launches": 0}
+
+
+def settle(step, ms: float):
+    """Runs `step` back to back until about `ms` of wall clock has passed,
+    before the warm-up steps.  A card that was idle runs its first launches
+    slow while its clocks ramp up (the 2 ms packed-prefill step takes 2.20 ms
+    at first and settles at 1.98 ms after about 8 steps), so the timed steps
+    start at the steady clock.  Nothing from these launches is timed or kept;
+    the totals go into the JSON line as "settle"."""
+    import torch
+    if ms <= 0:
+        return
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            step()
+        n += 4
+        torch.cuda.synchronize()
+    SETTLE["ms"] += (time.perf_counter() - t0) * 1e3
+    SETTLE["launches"] += n
+
+
 def calibrate_gemm(n: int, steps: int, warmup: int):
     """The practical bf16 MFMA ceiling on this card: hipBLASLt's n^3 GEMM
     (torch.matmul) on random N(0,1) operands and on all-zero operands.  The
@@ -222,6 +247,7 @@ def bench_gdn(args, w, dev, traffic_key: str):
     def fwd():
         layer(*xs, s_in=s_in, y=y, conv_out=conv_out, s_out=s_out)
 
+    settle(fwd, args.settle_ms)
     for _ in range(args.warmup):
         fwd()
     torch.cuda.synchronize()
@@ -259,6 +285,7 @@ def bench_gdn(args, w, dev, traffic_key: str):
         "roofline": roofline(w.flops(), alg, layer_ms, "f32", "gdn conv + prep + scan + norm (one forward call)",
                              traffic_from_profiles(traffic_key)),
         "device": device_info().name,
+        "settle": dict(SETTLE),
     }
     if args.cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_gdn(w, inp)
@@ -333,6 +360,7 @@ def bench_stack(args, w, dev):
         # values) and the code-head logits
         return stack.code_logits(stack.hidden(stack.run(tokens, pos, slots, table), gather), codes)
 
+    settle(step, args.settle_ms)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -366,6 +394,7 @@ def bench_stack(args, w, dev):
         "prefill_tflops": fl["prefill"] / (prefill_ms * 1e-3) / 1e12,
         "roofline": roofline(fl["pass"], 1, pass_ms, dt, "whole pass (library GEMMs + K1 + K2 + norms + SwiGLU)", None),
         "device": device_info().name,
+        "settle": dict(SETTLE),
     }
     res["roofline"]["alg_bytes"] = None
     if args.cpu_baseline:
@@ -373,13 +402,19 @@ def bench_stack(args, w, dev):
     print(json.dumps(res), flush=True)
 
 
-def time_layer(layer, steps: int, warmup: int, graph: bool):
+def time_layer(layer, steps: int, warmup: int, graph: bool, settle_ms: float = 0.0):
     """Times `steps` steps of one attention layer: K1, K2 and, for a d3
     workload, the readout of the last position, each bracketed by HIP events
     on the stream they launch on.  Returns (ms per step by the host clock,
     mean K1 ms, mean K2 ms, mean readout ms or None)."""
     import torch
     parts = [layer.qknorm, layer.attend] + ([layer.read_out] if layer.readout is not None else [])
+
+    def one_step():
+        for f in parts:
+            f()
+
+    settle(one_step, settle_ms)
     for _ in range(warmup):
         for f in parts:
             f()
@@ -429,6 +464,9 @@ def main():
     ap.add_argument("--hbm-shape", type=int, default=1,
                     help="with the default c3 workload, also time K2 on the 32k-prefix x 16-token shape (HBM-bound) "
                          "and report it under hbm_shape; 0 skips it")
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="run the step untimed for this long before the warm-up steps, so that timing starts at the "
+                         "card's steady clock (0 skips it)")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: capture each timed call once in a HIP graph and replay it; 0 (default): launch directly (graph launch costs more than it saves here)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -472,7 +510,7 @@ def main():
         return
     w = configs.WORKLOADS[args.workload]()
     layer = AttentionLayer(w, dev)
-    ms_step, k1_ms, k2_ms, k3_ms = time_layer(layer, args.steps, args.warmup, args.graph)
+    ms_step, k1_ms, k2_ms, k3_ms = time_layer(layer, args.steps, args.warmup, args.graph, args.settle_ms)
 
     dtype = "bf16" if w.bf16 else "f32"
     flops = w.useful_flops()
@@ -505,6 +543,7 @@ def main():
         "k2_ms": k2_ms,
         "roofline": roof,
         "device": device_info().name,
+        "settle": dict(SETTLE),
     }
     if k3_ms is not None:
         hidden, codes, temp = w.readout
