@@ -438,17 +438,17 @@ def time_layer(layer, steps: int, warmup: int, graph: bool, settle_ms: float = 0
     return ms_step, means[0], means[1], (means[2] if len(means) > 2 else None)
 
 
-def hbm_shape_record(dev, steps: int, warmup: int):
+def hbm_shape_record(dev, steps: int, warmup: int, settle_ms: float):
     """K2 on the long-prefix short-suffix shape (the 32768-key prefix with one
     16-token block), where the kernel streams K/V and HBM bandwidth bounds
     it: its mean time and the fraction of the 8 TB/s peak."""
     from cev_hip import configs
     from cev_hip.layer import AttentionLayer
     w = configs.hbm(1)
-    _, k1_ms, k2_ms, _ = time_layer(AttentionLayer(w, dev), steps, warmup, False)
+    _, k1_ms, k2_ms, _ = time_layer(AttentionLayer(w, dev), steps, warmup, False, settle_ms)
     gbps = w.alg_bytes() / (k2_ms * 1e-3) / 1e9
     return {"workload": f"{w.name}: {w.notes}", "k1_ms": k1_ms, "k2_ms": k2_ms, "alg_bytes": w.alg_bytes(),
-            "achieved_gbps": gbps, "peak_gbps": PEAK_HBM_GBPS, "frac": gbps / PEAK_HBM_GBPS,
+            "achieved_gbps": gbps, "peak_gbps": PEAK_HBM_GBPS, "frac": gbps / PEAK_HBM_GBPS, "settle_ms": settle_ms,
             "kernel": "attn_kernel_pipe<bf16,128> (split) + attn_merge_kernel"}
 
 
@@ -551,7 +551,7 @@ def main():
         res["config"]["readout"] = (f"d3 Kind::Matrix at the last position: o_proj ({w.hq * w.d} -> {hidden}), f32, "
                                     f"{codes} x {hidden} readout / temperature {temp}")
     if args.workload == "c3" and args.hbm_shape:
-        res["hbm_shape"] = hbm_shape_record(dev, args.steps, args.warmup)
+        res["hbm_shape"] = hbm_shape_record(dev, args.steps, args.warmup, args.settle_ms)
     if args.cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, layer.np_inputs)
     print(json.dumps(res), flush=True)
