@@ -51,6 +51,9 @@ struct AttnArgs {
 };
 
 constexpr float kRescale = 8.0f;
+// Largest sum of a lane's 16 probabilities of one sub-tile that the d = 128
+// loop accepts before it moves the row's max (so p < 2^16 there).
+constexpr float kMaxP = 65536.0f;
 
 // The plan header on the device must be the host plan's (same signature,
 // same launch shape).  A device plan that is not a copy of the validated
@@ -165,6 +168,14 @@ struct Frag<__bf16, D> {
       bf16x8 z = {};
       q[s] = ok ? *(const bf16x8*)(qp + 16 * s + 8 * u) : z;
     }
+  }
+  // q * c rounded to bf16: the QK^T MFMAs then give scores already in the
+  // base-2 units of the softmax (c = scale * log2 e).
+  __device__ __forceinline__ void scale_q(float c) {
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[s][e] = (__bf16)((float)q[s][e] * c);
   }
 
   // K operand of QK step st: key kt*32 + n, head-dim values 16st + 8u ..
@@ -409,6 +420,31 @@ __device__ __forceinline__ void load_chunk(const KvSource<T>& src, const Chunk& 
   }
 }
 
+// Query slot (wave, n = lane % 32) of a workgroup over tile rows [r0, r0 +
+// len) and KV head kvh holds tile row slot / g and query head slot % g: the
+// valid rows of a short tile fill the first waves.
+struct SlotRow {
+  int row, head, u;
+  bool ok;
+};
+__device__ __forceinline__ SlotRow slot_row(int lane, int wave, int kvh, int g, int r0, int len, int t) {
+  const int slot = wave * 32 + (lane & 31);
+  const int rit = slot / g;
+  SlotRow sr;
+  sr.ok = rit < len && r0 + rit < t;
+  sr.row = sr.ok ? r0 + rit : 0;
+  sr.head = kvh * g + slot % g;
+  sr.u = lane >> 5;
+  return sr;
+}
+
+// This lane's id, computed afresh (opaque to common-subexpression elimination).
+__device__ __forceinline__ int fresh_lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // --------------------------------------------------------------------------
 // bf16, d = 128: the MFMA and VALU halves of consecutive 32-key sub-tiles
 // overlap inside each wave (the loop below says how).  Two waves share a
@@ -575,24 +611,28 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   // Query slot (wave, n) holds row slot / g of the tile, query head slot % g:
   // the valid rows of a short tile fill the first waves, and a wave with no
   // valid row skips the MFMA work (it still fetches its share of K/V).
-  const int slot = wave * 32 + n;
-  const int gi = slot % a.g;
-  const int head = kvh * a.g + gi;
-  const int rit = slot / a.g;
-  const bool row_ok = rit < td.y && td.x + rit < a.t;
-  const int row = row_ok ? td.x + rit : 0;
+  const SlotRow sr0 = slot_row(lane, wave, kvh, a.g, td.x, td.y, a.t);
+  const bool row_ok = sr0.ok;
+  const int row = sr0.row, head = sr0.head;
   const bool wave_active = (wave * 32) / a.g < td.y;
-  const float c = a.scale_log2;
 
+  // Q arrives scaled by c = scale * log2 e, so an S^T tile holds base-2
+  // softmax arguments.  Each sub-tile's first QK^T MFMA starts from negm =
+  // -m_run instead of zero, so the tile comes out as c q.k - m_run and the
+  // probabilities are one exp2 per score.
   F fr;
   fr.load_q((const T*)a.q + (int64_t)row * a.q_st + (int64_t)head * a.q_sh, row_ok, u);
+  fr.scale_q(a.scale_log2);
   int4 rv = rows[row];
   if (!row_ok) rv = make_int4(0, 0, -1, 0);
 
   f32x16 o[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
-  float m_run = -1e30f, l_run = 0.0f;
+  // m_set: this row has seen a visible key, and m_run is a max it reached
+  // (0 until then); rows that never see one keep l = 0.
+  float m_run = 0.0f, l_run = 0.0f;
+  bool m_set = false;
 
   // ---- this part's slice of the tile's key stream: chunks [c0, c1)
   const int c0 = (int)((int64_t)part * n_chunks / a.n_splits);
@@ -714,9 +754,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
     wait_vmcnt<kLoadsPerChunk * (kAhead - 2)>();  // chunks 0 and 1 landed
     __builtin_amdgcn_s_barrier();
 
-    f32x16 sa, sb;
-    float mx = -INFINITY;  // lane-local max of the current sub-tile
+    f32x16 sa, sb, negm;
+    float mx = -INFINITY;  // lane-local max of the current sub-tile, relative to m_run
     if (wave_active) {
+      // Sub-tile 0 scored from zero: its row max (over both lane halves of
+      // the row) becomes m_run, and the tile is shifted by it.
       sa = f32x16{};
 #pragma unroll
       for (int st = 0; st < F::NQK; ++st) fr.qk_mfma(k_frag(0, 0, st), st, sa);
@@ -726,7 +768,15 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sa[i]);
       }
+      const float m0 = pair_max(mx);
+      m_set = m0 > -INFINITY;
+      m_run = m_set ? m0 : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sa[i] -= m_run;
+      mx -= m_run;
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) negm[i] = -m_run;
     // K reads in flight into the next body: the first body's are issued
     // here (sub-tile 1 of chunk 0) and waited for in full, so that its
     // counted waits see no fewer reads than a steady-state body's.
@@ -761,21 +811,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
           constexpr bool last = kt + 1 == NKT;
           constexpr int bn = last ? B1 : B0;  // buffer and sub-tile of the next scores
           constexpr int ktn = last ? 0 : kt + 1;
-          // lazy rescale against this sub-tile's row max
-          {
-            const float m_cand = pair_max(mx) * c;
-            const bool grow = m_cand > m_run + kRescale;
-            if (__ballot(grow)) {
-              const float m_new = grow ? m_cand : m_run;
-              const float alpha = fast_exp2(m_run - m_new);
-              m_run = m_new;
-              l_run *= alpha;
-#pragma unroll
-              for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
-            }
-          }
-          const float mc = -m_run;
-          float rs = 0.0f, m2 = -INFINITY;
+          float rs = 0.0f;
           constexpr int KPF = kKPF, VPF = kVPF;
           // Each unit below ends in a scheduling fence, so the order is the
           // program order unit by unit: one MFMA of one stream next to the
@@ -787,19 +823,21 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
           using KTN_c = std::integral_constant<int, ktn>;
           VFrag vf[VPF];
           P p;
-          sn = f32x16{};
           const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-          // Region A: QK(j+1) on the MFMA unit; exp(j), P(j) and its row sum
-          // on the VALU, two probabilities per unit.  Its last VPF units
-          // issue the first V fragments of region B.
+          // Region A: QK(j+1) on the MFMA unit (from negm); exp2(j), P(j) and
+          // its row sum on the VALU, two probabilities per unit.  Its last
+          // VPF units issue the first V fragments of region B.
           static_for<F::NQK>([&](auto st_c) {
             constexpr int st = decltype(st_c)::value;
-            fr.qk_mfma(k_ready(kf[st % KPF], st_c), st, sn);
+            if constexpr (st == 0)
+              sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_ready(kf[0], st_c), fr.q[0], negm, 0, 0, 0);
+            else
+              fr.qk_mfma(k_ready(kf[st % KPF], st_c), st, sn);
             if constexpr (st + KPF < F::NQK) kf[st % KPF] = k_issue(BN_c{}, KTN_c{}, std::integral_constant<int, st + KPF>{});
             if constexpr (st >= F::NQK - VPF)
               vf[st - (F::NQK - VPF)] = v_issue(std::integral_constant<int, B0>{}, kt_c, std::integral_constant<int, st - (F::NQK - VPF)>{});
-            const float e0 = fast_exp2(__builtin_fmaf(s[2 * st], c, mc));
-            const float e1 = fast_exp2(__builtin_fmaf(s[2 * st + 1], c, mc));
+            const float e0 = fast_exp2(s[2 * st]);
+            const float e1 = fast_exp2(s[2 * st + 1]);
             const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
             p.h[st / 4][2 * (st % 4)] = pr[0];
             p.h[st / 4][2 * (st % 4) + 1] = pr[1];
@@ -807,7 +845,42 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
             pin(rs);
             __builtin_amdgcn_sched_barrier(0);
           });
-          // Region B: PV(j) on the MFMA unit, row max of S(j+1) on the VALU.
+          // Lazy max: S(j) came out relative to m_run, and its probabilities
+          // stand as long as their row sum stays within kMaxP (O and l are
+          // f32).  Otherwise, or for a row with no max yet, the row moves its
+          // max (a set row only when it grew by more than kRescale) and P(j)
+          // is made again.  This branch issues no LDS operation, so the
+          // counted waits of region B still hold.
+          if (__ballot((rs > kMaxP) | !m_set)) {
+            float ml = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ml = fmaxf(ml, s[i]);
+            const float delta = pair_max(ml);
+            const bool move = m_set ? delta > kRescale : delta > -INFINITY;
+            const float dm = move ? delta : 0.0f;
+            const float alpha = m_set ? fast_exp2(-dm) : 1.0f;
+            m_set = m_set | move;
+            m_run += dm;
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+            rs = 0.0f;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int j = 0; j < 8; j += 2) {
+                const bf16x2 pr = {(__bf16)fast_exp2(s[8 * h + j] - dm), (__bf16)fast_exp2(s[8 * h + j + 1] - dm)};
+                p.h[h][j] = pr[0];
+                p.h[h][j + 1] = pr[1];
+                rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
+              }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              sn[i] -= dm;
+              negm[i] = -m_run;
+            }
+          }
+          // Region B: PV(j) on the MFMA unit.
           static_for<F::NPV>([&](auto j_c) {
             constexpr int j = decltype(j_c)::value;
             F::pv_mfma(v_ready(vf[j % VPF], j_c), j, p, o);
@@ -818,15 +891,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
               kf[j - (F::NPV - KPF)] = k_issue(std::integral_constant<int, (B0 + (kt + 2) / 2) % kBuf>{},
                                                std::integral_constant<int, (kt + 2) % 2>{},
                                                std::integral_constant<int, j - (F::NPV - KPF)>{});
-            m2 = fmaxf(m2, fmaxf(sn[2 * j], sn[2 * j + 1]));
-            pin(m2);
             __builtin_amdgcn_sched_barrier(0);
           });
           l_run += rs;
-          mx = m2;
           if (!last || has1) {
             const Chunk& chn = last ? chs[1] : chs[0];
-            if (needs_mask(chn)) mx = mask_sub(sn, ktn, chn);
+            if (needs_mask(chn)) mask_sub(sn, ktn, chn);
           }
         });
       }
@@ -855,28 +925,33 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   }
 
   const float l = pair_sum(l_run);
-  if (!row_ok) return;
+  // The slot's row and head again, from a lane id the compiler cannot
+  // match with the one above, so they are not kept (spilled) across the loop.
+  const SlotRow sr = slot_row(fresh_lane_id(), wave, kvh, a.g, td.x, td.y, a.t);
+  if (!sr.ok) return;
+  const int ue = sr.u;
   if (a.n_splits > 1) {
     // Partial record: O unnormalised, then m and l.
-    float* rec = a.ws + (((int64_t)row * a.hq + head) * a.n_splits + part) * cev_attn_partial_floats(D);
+    float* rec = a.ws + (((int64_t)sr.row * a.hq + sr.head) * a.n_splits + part) * cev_attn_partial_floats(D);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = dt * 32 + 8 * q4 + 4 * u;
+        const int d = dt * 32 + 8 * q4 + 4 * ue;
         *(f32x4*)(rec + d) = f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
       }
-    if (u == 0) *(f32x4*)(rec + D) = f32x4{m_run, l, 0.0f, 0.0f};
+    // a row that saw no key (l = 0) records the finite m of an empty part
+    if (ue == 0) *(f32x4*)(rec + D) = f32x4{l > 0.0f ? m_run : -1e30f, l, 0.0f, 0.0f};
     return;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
-  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh : nullptr;
+  T* op = (T*)a.out + (int64_t)sr.row * a.o_st + (int64_t)sr.head * a.o_sh;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)sr.row * a.g_st + (int64_t)sr.head * a.g_sh : nullptr;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = dt * 32 + 8 * q4 + 4 * u;
+      const int d = dt * 32 + 8 * q4 + 4 * ue;
       float v[4], gv[4];
       if (gp) load_vec4<T>(gp + d, gv);
 #pragma unroll

@@ -239,6 +239,56 @@ def test_small_packed_passes(gpu, orc, case):
     assert err <= (BF16_TOL if bf else F32_TOL)
 
 
+@pytest.mark.parametrize("shape", ["ramp", "spike", "low", "unseen_first"])
+@pytest.mark.parametrize("max_splits", [1, 0])
+def test_softmax_max_moves(gpu, orc, shape, max_splits):
+    """Scores far from the first key tile's: the kernels move a row's max
+    lazily, so these drive every move (d = 128 and 256, bf16 and f32).
+    ramp: scores climb by about 100 (base 2) over the prefix, so the row max
+    moves many times and unmoved probabilities would overflow; spike: one key
+    about 60 above the rest, late in the stream; low: every score near -150,
+    where probabilities against a max of 0 would underflow; unseen_first: a
+    causal block with no prefix, split so that parts start on keys some rows
+    cannot see.  bf16 is held to exact (f64) attention: at these score
+    magnitudes the candle-op restatement's own bf16 rounding of the scores
+    moves its result by more than the bar; f32 is held to both."""
+    rng = np.random.default_rng(7)
+    for bf, d, hq, hkv in [(True, 128, 8, 2), (True, 256, 8, 2), (False, 128, 4, 2)]:
+        P, L = (0, 300) if shape == "unseen_first" else (2048, 40)
+        u = rng.standard_normal(d).astype(np.float32)
+        u /= np.linalg.norm(u)
+        q = (0.2 * rng.standard_normal((L, hq, d)) + 8.0 * u).astype(np.float32)
+        kc = 0.2 * rng.standard_normal((hkv, P, d)).astype(np.float32)
+        if shape == "ramp":
+            kc += (np.linspace(-2.0, 100.0, P, dtype=np.float32)[None, :, None] * u)
+        elif shape == "spike":
+            kc[:, 1500] += 60.0 * u
+        elif shape == "low":
+            kc -= 150.0 * u
+        vc = rng.standard_normal((hkv, P, d)).astype(np.float32)
+        kn = (0.2 * rng.standard_normal((L, hkv, d)) + rng.uniform(-3, 3, (L, 1, 1)) * u).astype(np.float32)
+        vn = rng.standard_normal((L, hkv, d)).astype(np.float32)
+        rnd = (lambda x: orc.round_bf16(x)) if bf else (lambda x: x)
+        q, kc, vc, kn, vn = map(rnd, (q, kc, vc, kn, vn))
+        tab = cev_hip.BlockTable.from_rows(1, L, P, causal=True)
+        dev = lambda x: to_dev(x, bf, gpu)  # noqa: E731
+        out = cev_hip.packed_attention(dev(q), dev(kn), dev(vn), tab, k_cache=dev(kc) if P else None,
+                                       v_cache=dev(vc) if P else None, max_splits=max_splits)
+        got = to_np(out)
+        kall = np.concatenate([kc, kn.transpose(1, 0, 2)], axis=1)
+        vall = np.concatenate([vc, vn.transpose(1, 0, 2)], axis=1)
+        mask = orc.branch_mask(L, P)
+        want = orc.attend(q.transpose(1, 0, 2), kall, vall, mask, bf)[0].transpose(1, 0, 2)
+        want64 = orc.attend_f64(q.transpose(1, 0, 2), kall, vall, mask)[0].transpose(1, 0, 2)
+        assert np.isfinite(got).all()
+        err, err64 = float(np.abs(got - want).max()), float(np.abs(got - want64).max())
+        _say(f"{shape} bf16={bf} d={d} splits={max_splits}: max|d| {err:.3g} (f64 {err64:.3g}), max|out| {np.abs(want).max():.3g}")
+        if bf:
+            assert err64 <= BF16_TOL
+        else:
+            assert err <= F32_TOL and err64 <= F32_TOL
+
+
 def test_packed_equals_each_block_alone_on_gpu(gpu):
     """qwen3.rs:13-17: packing is exactly asking each question alone.  The
     kernel visits the same key tiles in the same order either way (unsplit),
