@@ -12,7 +12,8 @@ Prints one JSON line: query tokens/s (value), TFLOP/s, the roofline record of
 K2 (its average launch time from HIP events on its stream), the CPU baseline
 (the oracle's candle-op restatement on a bounded sample, timed on this
 host's cores) and, for the default workload, K2 on the HBM-bound
-32k-prefix x 16-token shape under hbm_shape (outside the timed steps).
+32k-prefix x 16-token shape under hbm_shape and K2 on config 4's d = 256
+bidirectional row under c4_shape (both outside the timed steps).
 """
 import argparse
 import json
@@ -32,14 +33,30 @@ PEAK_TFLOPS = {"bf16": 2516.6, "f32": 157.3}   # dense MFMA at 2.4 GHz
 PEAK_HBM_GBPS = 8000.0
 
 
+# Kernel source each workload's measured traffic depends on.
+TRAFFIC_SOURCES = {"c5gdn": "gdn.hip", "c5gdnrows": "gdn.hip"}
+
+
+def source_sha16(name: str) -> str:
+    """First 16 hex digits of the SHA-256 of rust-cev_amd/csrc/<name>."""
+    import hashlib
+    with open(os.path.join(ROOT, "rust-cev_amd", "csrc", name), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per K2 launch (or per GDN forward call) measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by a copy-kernel calibration), if recorded."""
+    WRITE_SIZE, scaled by a copy-kernel calibration), if recorded for the kernel source in the tree:
+    each recorded value names the SHA-256 prefix of the source it was measured on, and a value
+    measured on another version of the kernel is not reported (None)."""
     path = os.path.join(ROOT, "profiles", "packed_attn_traffic.md")
     if not os.path.exists(path):
         return None
-    m = re.search(r"traffic\[%s\]\s*=\s*([0-9.]+)" % re.escape(workload), open(path).read())
-    return float(m.group(1)) if m else None
+    m = re.search(r"traffic\[%s\]\s*=\s*([0-9.]+)\s+src=([0-9a-f]{16})" % re.escape(workload), open(path).read())
+    if not m:
+        return None
+    src = TRAFFIC_SOURCES.get(workload, "packed_attn.hip")
+    return float(m.group(1)) if m.group(2) == source_sha16(src) else None
 
 
 def cpu_model() -> str:
@@ -226,7 +243,7 @@ def bench_gdn(args, w, dev, traffic_key: str):
     import torch
 
     import cev_hip
-    from cev_hip import device_info
+    from cev_hip import configs, device_info
     inp = w.inputs()
     mdt = torch.bfloat16 if w.bf16 else torch.float32
 
@@ -238,14 +255,26 @@ def bench_gdn(args, w, dev, traffic_key: str):
 
     layer = cev_hip.GatedDeltaNet(w.batch, w.t, w.nk, w.nv, w.dk, w.dv, w.kernel, w.eps, dtype=mdt, device=dev)
     xs = [d(inp[k]) for k in ("mixed", "z", "b", "a", "conv_w")] + [f(inp[k]) for k in ("neg_a", "dt_bias", "norm_w")]
-    s_in = None
+    s_in = conv_in = None
+    prefill = None
     if w.batch > 1:
-        s_in = torch.zeros((1, w.nv, w.dk, w.dv), device=dev).expand(w.batch, -1, -1, -1)
+        # The rows continue from config 5's 4096-token prefill (hybrid.rs:554-617):
+        # its conv tail and recurrent state, computed once here outside the
+        # timed steps, are read by every row through batch stride 0.
+        pw = configs.c5_gdn()
+        pinp = pw.inputs()
+        player = cev_hip.GatedDeltaNet(1, pw.t, pw.nk, pw.nv, pw.dk, pw.dv, pw.kernel, pw.eps, dtype=mdt, device=dev)
+        pxs = [d(pinp[k]) for k in ("mixed", "z", "b", "a")] + [xs[4]] + xs[5:]
+        _, pconv, pstate = player(*pxs)
+        conv_in = pconv.expand(w.batch, -1, -1)
+        s_in = pstate.expand(w.batch, -1, -1, -1)
+        prefill = f"state from the {pw.t}-token prefill ({pw.name}), computed once before the timed steps"
+        del player
     y = torch.empty((w.batch, w.t, w.nv * w.dv), dtype=mdt, device=dev)
     conv_out = torch.empty((w.batch, w.conv_dim, w.kernel - 1), dtype=mdt, device=dev)
     s_out = torch.empty((w.batch, w.nv, w.dk, w.dv), dtype=torch.float32, device=dev)
     def fwd():
-        layer(*xs, s_in=s_in, y=y, conv_out=conv_out, s_out=s_out)
+        layer(*xs, conv_in=conv_in, s_in=s_in, y=y, conv_out=conv_out, s_out=s_out)
 
     settle(fwd, args.settle_ms)
     for _ in range(args.warmup):
@@ -268,8 +297,11 @@ def bench_gdn(args, w, dev, traffic_key: str):
     layer_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
     esz = 2 if w.bf16 else 4
     tok = w.batch * w.t
-    alg = (tok * (w.conv_dim + 2 * w.nv * w.dv + 2 * w.nv) * esz + w.batch * w.nv * w.dk * w.dv * 4 * (2 if s_in is not None else 1)
-           + w.batch * w.conv_dim * (w.kernel - 1) * esz)
+    # inputs and y once per token, every row's new state and conv tail, and
+    # the one broadcast initial state and tail the rows read
+    state, tail = w.nv * w.dk * w.dv * 4, w.conv_dim * (w.kernel - 1) * esz
+    alg = (tok * (w.conv_dim + 2 * w.nv * w.dv + 2 * w.nv) * esz + w.batch * (state + tail)
+           + ((state + tail) if s_in is not None else 0))
     res = {
         "metric": "Gated DeltaNet layer core tok/s and % f32 MFMA peak on 1 MI355X",
         "value": tok / (ms_step * 1e-3),
@@ -281,7 +313,8 @@ def bench_gdn(args, w, dev, traffic_key: str):
         "config": {"workload": f"{w.name}: Gated DeltaNet layer, batch {w.batch} x {w.t} tokens, Hk={w.nk} Hv={w.nv} "
                                f"dk={w.dk} dv={w.dv}, conv kernel {w.kernel}, 64-token chunks, "
                                f"{'bf16' if w.bf16 else 'f32'} inputs, f32 chunk rule",
-                   "launch": "hip graph replay" if args.graph else "direct launches"},
+                   "launch": "hip graph replay" if args.graph else "direct launches",
+                   **({"initial_state": prefill} if prefill else {})},
         "roofline": roofline(w.flops(), alg, layer_ms, "f32", "gdn conv + prep + scan + norm (one forward call)",
                              traffic_from_profiles(traffic_key)),
         "device": device_info().name,
@@ -452,6 +485,21 @@ def hbm_shape_record(dev, steps: int, warmup: int, settle_ms: float):
             "kernel": "attn_kernel_pipe<bf16,128> (split) + attn_merge_kernel"}
 
 
+def c4_shape_record(dev, steps: int, warmup: int, settle_ms: float):
+    """K2 on config 4 (the Qwen3.5-style gated layer, d = 256, one
+    bidirectional 8192-token row): the d = 256 kernel's mean time, useful
+    TFLOP/s and fraction of the bf16 MFMA peak.  K1 and the d3 readout are
+    timed with it and reported beside."""
+    from cev_hip import configs
+    from cev_hip.layer import AttentionLayer
+    w = configs.c4()
+    _, k1_ms, k2_ms, k3_ms = time_layer(AttentionLayer(w, dev), steps, warmup, False, settle_ms)
+    roof = roofline(w.useful_flops(), w.alg_bytes(), k2_ms, "bf16", "attn_kernel_wide<bf16,256>", traffic_from_profiles(w.name))
+    return {"workload": f"{w.name}: {w.notes}", "k1_ms": k1_ms, "k2_ms": k2_ms, "readout_ms": k3_ms,
+            "useful_flop": roof["useful_flop"], "achieved_tflops": roof["achieved"], "peak_tflops": roof["peak"],
+            "frac": roof["frac"], "settle_ms": settle_ms, "kernel": roof["kernel"]}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -464,6 +512,9 @@ def main():
     ap.add_argument("--hbm-shape", type=int, default=1,
                     help="with the default c3 workload, also time K2 on the 32k-prefix x 16-token shape (HBM-bound) "
                          "and report it under hbm_shape; 0 skips it")
+    ap.add_argument("--c4-shape", type=int, default=1,
+                    help="with the default c3 workload, also time K2 on config 4 (d = 256, bidirectional 8192-token "
+                         "gated row, MFMA-bound) and report it under c4_shape; 0 skips it")
     ap.add_argument("--settle-ms", type=float, default=200.0,
                     help="run the step untimed for this long before the warm-up steps, so that timing starts at the "
                          "card's steady clock (0 skips it)")
@@ -497,7 +548,7 @@ def main():
         bench_stack(args, configs.c2(True), dev)
         return
     if args.workload == "c5gdnrows":
-        bench_gdn(args, configs.GdnWorkload("c5gdn32x64", 5, True, 32, 64), dev, "c5gdnrows")
+        bench_gdn(args, configs.c5_gdn_rows(), dev, "c5gdnrows")
         return
     if args.calibrate_copy:
         n = args.calibrate_copy << 20
@@ -552,6 +603,8 @@ def main():
                                     f"{codes} x {hidden} readout / temperature {temp}")
     if args.workload == "c3" and args.hbm_shape:
         res["hbm_shape"] = hbm_shape_record(dev, args.steps, args.warmup, args.settle_ms)
+    if args.workload == "c3" and args.c4_shape:
+        res["c4_shape"] = c4_shape_record(dev, args.steps, args.warmup, args.settle_ms)
     if args.cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, layer.np_inputs)
     print(json.dumps(res), flush=True)

@@ -156,9 +156,14 @@ int32_t cev_packed_attention(const cev_attn_desc* d, const void* plan_host, cons
  * device buffer of CEV_ATTN_SCRATCH_BYTES inside the library (one per GPU,
  * held until the process ends) instead of a caller workspace: a plan whose
  * cev_attn_workspace_size exceeds it fails with CEV_ERR_SPACE.  It calls no
- * hipMalloc / hipFree.  Every call on one GPU shares that buffer: calls
- * that overlap in time on one GPU (several streams or threads) race and
- * must be serialised by the caller. */
+ * hipMalloc / hipFree.  The first call on each device that needs the buffer
+ * looks up its device address (hipGetSymbolAddress): make that call once
+ * outside HIP graph capture (a warm-up); later calls, captured or not, make
+ * no runtime call besides the launches.  Every call on one GPU shares the
+ * buffer: calls that overlap in time on one GPU (several streams or
+ * threads) race and must be serialised by the caller.  A call made while
+ * another host thread is inside this function for the same device fails
+ * with CEV_ERR_SPACE; work already queued on other streams is not seen. */
 #define CEV_ATTN_SCRATCH_BYTES ((size_t)64 << 20)
 int32_t cev_packed_attention_noalloc(const cev_attn_desc* d, const void* plan_host, const void* plan_dev, const void* q,
                                      const void* k_cache, const void* v_cache, const void* k_new, const void* v_new, const void* gate,
@@ -319,7 +324,9 @@ int32_t cev_blas_destroy(cev_blas handle);
  * or dtype); f32 accumulation, one rounding to the output dtype.  m <= 8
  * runs this library's own kernel (handle may be NULL, no workspace); larger
  * m a hipBLASLt GEMM on `handle` with the caller's workspace
- * (CEV_LINEAR_WORKSPACE_BYTES recommended; 0 allowed). */
+ * (CEV_LINEAR_WORKSPACE_BYTES recommended; 0 allowed).  x and w must be
+ * 16-byte aligned with ldx, ldw multiples of 8 (bf16) or 4 (f32) elements;
+ * for m > 8 the same holds for y and ldy in the output dtype. */
 #define CEV_LINEAR_WORKSPACE_BYTES ((size_t)32 << 20)
 int32_t cev_linear(cev_blas handle, int32_t dtype, int32_t out_dtype, int64_t m, int64_t n, int64_t k, const void* x, int64_t ldx,
                    const void* w, int64_t ldw, float alpha, void* y, int64_t ldy, void* workspace, size_t workspace_bytes,

@@ -224,6 +224,13 @@ def c5_gdn(t: int = 4096, batch: int = 1) -> GdnWorkload:
     return GdnWorkload(f"c5gdn{batch}x{t}", 5, True, batch, t)
 
 
+def c5_gdn_rows() -> GdnWorkload:
+    """Config 5's 32 question rows right-padded to 64 tokens through the GDN
+    layer, continuing from the 4096-token prefill's state (their own seed,
+    so their tokens are not the prefill's first tokens again)."""
+    return GdnWorkload("c5gdn32x64", 55, True, 32, 64)
+
+
 @dataclass
 class Qwen3StackWorkload:
     """Config 2: a Qwen3-1.7B-shaped decoder stack (28 layers, hidden 2048,

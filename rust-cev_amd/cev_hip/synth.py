@@ -45,29 +45,32 @@ def uniform(seed: int, stream: int, n: int, lo: float = 0.0, hi: float = 1.0) ->
 
 
 def normal(seed: int, stream: int, n: int) -> np.ndarray:
-    """n standard normals (f64) by Box-Muller on consecutive uniform pairs."""
+    """n standard normals (f64) by Box-Muller on consecutive uniform pairs:
+    element 2j is r cos(a) and element 2j+1 is r sin(a) of pair j."""
     key = _key(seed, stream)
     out = np.empty(n, np.float64)
-    for s in range(0, n, _CHUNK):
+    for s in range(0, n, _CHUNK):  # _CHUNK is even, so every chunk starts on a pair
         e = min(n, s + _CHUNK)
-        i = np.arange(s, e, dtype=np.uint64)
-        pair = i // np.uint64(2)
-        u1 = (_u64(key, pair * np.uint64(2)) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
-        u2 = (_u64(key, pair * np.uint64(2) + np.uint64(1)) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
-        r = np.sqrt(-2.0 * np.log1p(-u1))
-        ang = 2.0 * np.pi * u2
-        out[s:e] = np.where((i & np.uint64(1)) == 0, r * np.cos(ang), r * np.sin(ang))
+        u = (_u64(key, np.arange(s, e + (e - s) % 2, dtype=np.uint64)) >> np.uint64(11)).astype(np.float64)
+        u *= 1.0 / 9007199254740992.0
+        r = np.sqrt(-2.0 * np.log1p(-u[0::2]))
+        ang = 2.0 * np.pi * u[1::2]
+        both = np.empty(u.size, np.float64)
+        both[0::2] = r * np.cos(ang)
+        both[1::2] = r * np.sin(ang)
+        out[s:e] = both[:e - s]
     return out
 
 
 def round_bf16(x: np.ndarray) -> np.ndarray:
     """f32 array holding the round-to-nearest-even bf16 value of each element."""
     x = np.ascontiguousarray(x, np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    nan = (u & np.uint64(0x7FFFFFFF)) > np.uint64(0x7F800000)
-    r = ((u + np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))) & np.uint64(0xFFFF0000))
-    r = np.where(nan, (u | np.uint64(0x00400000)) & np.uint64(0xFFFF0000), r)
-    return r.astype(np.uint32).view(np.float32).reshape(x.shape)
+    u = x.view(np.uint32)
+    nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    # no wrap-around for non-NaN values: |bits| <= 0x7F800000 before the sign
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    r = np.where(nan, (u | np.uint32(0x00400000)) & np.uint32(0xFFFF0000), r)
+    return r.view(np.float32).reshape(x.shape)
 
 
 def tensor(seed: int, stream: int, shape, bf16: bool, scale: float = 1.0, offset: float = 0.0) -> np.ndarray:

@@ -282,6 +282,12 @@ extern "C" int32_t cev_linear(cev_blas handle, int32_t dtype, int32_t out_dtype,
     if (dtype == CEV_BF16) return launch_rows<uint16_t>(a, out_dtype, s);
     return launch_rows<float>(a, out_dtype, s);
   }
+  // The hipBLASLt algorithm is chosen once per shape and kept, so every
+  // operand of that path meets the same alignment (the cached choice never
+  // meets a less aligned y than it was chosen for).
+  const int ovec = out_dtype == CEV_BF16 ? 8 : 4;
+  CEV_CHECK_ARG(aligned16(y) && ldy % ovec == 0, "cev_linear: with more than %d rows y must be 16-byte aligned and ldy a multiple of %d",
+                kRowsSmall, ovec);
   CEV_CHECK_ARG(handle != nullptr, "cev_linear: more than %d rows need a cev_blas handle", kRowsSmall);
   CEV_CHECK_ARG(workspace_bytes == 0 || workspace != nullptr, "cev_linear: null workspace of %zu bytes", workspace_bytes);
   Blas* b = (Blas*)handle;

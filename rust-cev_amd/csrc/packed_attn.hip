@@ -1708,12 +1708,20 @@ int32_t packed_attention_impl(const cev_attn_desc* d, const void* plan_host, con
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mu;
+// Host threads inside cev_packed_attention_noalloc per device: a second
+// thread that enters while another is launching on the same device is
+// refused, since their launches would share the buffer.
+std::atomic<int> g_scratch_users[kMaxDevices];
 
-int32_t scratch_ptr(void** out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+int32_t current_device(int* dev) {
+  hipError_t e = hipGetDevice(dev);
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
-  if (dev < 0 || dev >= kMaxDevices) return cev_fail(CEV_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", dev, kMaxDevices);
+  if (*dev < 0 || *dev >= kMaxDevices) return cev_fail(CEV_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", *dev, kMaxDevices);
+  return CEV_OK;
+}
+
+int32_t scratch_ptr(int dev, void** out) {
+  hipError_t e;
   void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
   if (!p) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -1748,11 +1756,21 @@ extern "C" int32_t cev_packed_attention_noalloc(const cev_attn_desc* d, const vo
   if (need > kScratchBytes)
     return cev_fail(CEV_ERR_SPACE, "cev_packed_attention_noalloc: the plan needs %zu bytes of split records, the static scratch holds %zu",
                     need, kScratchBytes);
-  void* ws = nullptr;
-  if (need > 0) {
-    rc = scratch_ptr(&ws);
-    if (rc) return rc;
+  if (need == 0)
+    return packed_attention_impl(d, plan_host, plan_dev, q, k_cache, v_cache, k_new, v_new, gate, out, nullptr, 0, stream);
+  int dev = 0;
+  rc = current_device(&dev);
+  if (rc) return rc;
+  if (g_scratch_users[dev].fetch_add(1, std::memory_order_acq_rel) != 0) {
+    g_scratch_users[dev].fetch_sub(1, std::memory_order_acq_rel);
+    return cev_fail(CEV_ERR_SPACE,
+                    "cev_packed_attention_noalloc: another thread is launching on device %d's static scratch; calls that "
+                    "share it must be serialised",
+                    dev);
   }
-  return packed_attention_impl(d, plan_host, plan_dev, q, k_cache, v_cache, k_new, v_new, gate, out, ws, need > 0 ? kScratchBytes : 0,
-                               stream);
+  void* ws = nullptr;
+  rc = scratch_ptr(dev, &ws);
+  if (!rc) rc = packed_attention_impl(d, plan_host, plan_dev, q, k_cache, v_cache, k_new, v_new, gate, out, ws, kScratchBytes, stream);
+  g_scratch_users[dev].fetch_sub(1, std::memory_order_acq_rel);
+  return rc;
 }

@@ -206,6 +206,16 @@ def test_linear_gather_and_kv_store_validation(cev):
     assert lin(CEV_BF16, CEV_F32, 2, 4, 64, p, 64, p, 64, 1.0, p, 2) == CEV_ERR_INVALID       # ldy < n
     assert lin(CEV_BF16, CEV_F32, 2, 4, 64, odd, 64, p, 64, 1.0, p, 4) == CEV_ERR_INVALID
     assert lin(CEV_BF16, CEV_F32, 16, 4, 64, p, 64, p, 64, 1.0, p, 4) == CEV_ERR_INVALID      # 16 rows, no handle
+    # the library GEMM path (more than 8 rows) needs y 16-byte aligned and ldy
+    # a multiple of the output's 16-byte vector, checked before the handle
+    assert lin(CEV_BF16, CEV_F32, 16, 4, 64, p, 64, p, 64, 1.0, odd, 4) == CEV_ERR_INVALID
+    assert "y must be 16-byte aligned" in L.cev_last_error().decode()
+    assert lin(CEV_BF16, CEV_F32, 16, 4, 64, p, 64, p, 64, 1.0, p, 6) == CEV_ERR_INVALID      # ldy 6 f32
+    assert "y must be 16-byte aligned" in L.cev_last_error().decode()
+    assert lin(CEV_BF16, CEV_BF16, 16, 8, 64, p, 64, p, 64, 1.0, p, 12) == CEV_ERR_INVALID    # ldy 12 bf16
+    assert "y must be 16-byte aligned" in L.cev_last_error().decode()
+    assert lin(CEV_BF16, CEV_F32, 16, 4, 64, p, 64, p, 64, 1.0, p, 8) == CEV_ERR_INVALID      # aligned: only the handle is missing
+    assert "cev_blas handle" in L.cev_last_error().decode()
     assert lin(CEV_BF16, CEV_F32, 0, 4, 64, None, 0, None, 0, 1.0, None, 0) == 0               # nothing to do
     gat = lambda dt, odt, n, width, table, ldt, rows, ids, out, ldo: L.cev_gather_rows(  # noqa: E731
         dt, odt, n, width, table, ldt, rows, ids, out, ldo, None)

@@ -2,7 +2,10 @@
 
 Bars (from the path's contract): attention output max |delta| <= 1e-5 in f32
 and <= 2e-2 in bf16 against the candle-op restatement on identical seeded
-inputs.  The QK-norm + RoPE prologue is checked bit for bit.  c1, c3 and c5a
+inputs; every bf16 comparison is also held relative to the largest reference
+value (tests/bars.py: 3e-2 against the candle-op restatement, 2e-2 against
+exact attention), which a dropped key chunk, a shifted position or a missing
+gate would miss at these output scales.  The QK-norm + RoPE prologue is checked bit for bit.  c1, c3 and c5a
 are compared in full, and c4's 8192-token row against the candle-op
 restatement in full; the f64 textbook covers every c1 and c5a block, three c3
 blocks and 512 c4 rows.  Size-independent properties (packed == each block
@@ -13,12 +16,13 @@ import pytest
 
 import cev_hip
 from cev_hip import configs
+from bars import BF16_ABS, F32_ABS, assert_bf16, assert_f32, errors
 from helpers import GpuLayer, OracleLayer, default_table, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
-F32_TOL = 1e-5
-BF16_TOL = 2e-2
+F32_TOL = F32_ABS
+BF16_TOL = BF16_ABS
 
 
 def _say(msg):
@@ -29,25 +33,29 @@ def _check_blocks(gl, ol, blocks, tol, rows=None):
     import torch
     torch.cuda.synchronize()
     out = to_np(gl.out)
-    worst = 0.0
-    worst64 = 0.0
+    worst = worst64 = rel = rel64 = 0.0
     for b in blocks:
         r0 = int(gl.w.block_starts()[b])
         L = gl.w.blocks[b]
-        want = ol.block(b, rows=rows)
-        got = out[r0:r0 + L]
         sel = slice(None) if rows is None else slice(rows[0], rows[0] + rows[1])
-        err = float(np.abs(got[sel] - want[sel]).max())
-        assert np.isfinite(got[sel]).all()
-        worst = max(worst, err)
-        w64 = ol.block(b, rows=rows, f64=True)
-        worst64 = max(worst64, float(np.abs(got[sel] - w64[sel]).max()))
-    _say(f"{gl.w.name}: max|d| vs candle-op oracle {worst:.3g}, vs f64 textbook {worst64:.3g}")
-    assert worst <= tol, worst
-    # Against exact attention (f64, no model-dtype rounding) the same bar
-    # holds: in bf16 the reference's own rounding of scores and
-    # probabilities moves it by well under 1e-3 at these shapes.
-    assert worst64 <= tol, worst64
+        got = out[r0:r0 + L][sel]
+        want = ol.block(b, rows=rows)[sel]
+        w64 = ol.block(b, rows=rows, f64=True)[sel]
+        assert np.isfinite(got).all()
+        e, r = errors(got, want)
+        e64, r64 = errors(got, w64)
+        worst, worst64, rel, rel64 = max(worst, e), max(worst64, e64), max(rel, r), max(rel64, r64)
+        # The same bars hold against exact attention (f64, no model-dtype
+        # rounding): the reference's own bf16 rounding moves it by well
+        # under them at these shapes.
+        if gl.w.bf16:
+            assert_bf16(got, candle=want, exact=w64, what=f"{gl.w.name} block {b}")
+        else:
+            assert_f32(got, want, f"{gl.w.name} block {b}")
+            assert_f32(got, w64, f"{gl.w.name} block {b} vs f64")
+    _say(f"{gl.w.name}: max|d| vs candle-op oracle {worst:.3g} ({rel:.3g} of max|ref|), vs f64 textbook {worst64:.3g} "
+         f"({rel64:.3g})")
+    assert worst <= tol and worst64 <= tol, (worst, worst64)
     return worst
 
 
@@ -86,14 +94,15 @@ def test_c3_bf16_every_block_every_head(gpu, orc):
     gl.forward()
     torch.cuda.synchronize()
     out = to_np(gl.out)
-    worst = 0.0
+    worst = rel = 0.0
     for b in range(len(w.blocks)):
         r0, L = int(w.block_starts()[b]), w.blocks[b]
         got = out[r0:r0 + L]
-        assert np.isfinite(got).all()
-        worst = max(worst, float(np.abs(got - ol.block(b)).max()))
-    _say(f"  {len(w.blocks)} blocks: max|d| {worst:.3g}")
-    assert worst <= BF16_TOL
+        want = ol.block(b)
+        e, r = errors(got, want)
+        worst, rel = max(worst, e), max(rel, r)
+        assert_bf16(got, candle=want, what=f"c3 block {b}")
+    _say(f"  {len(w.blocks)} blocks: max|d| {worst:.3g} ({rel:.3g} of max|ref|)")
 
 
 def test_c4_bidirectional_gated_full_row(gpu, orc):
@@ -110,10 +119,10 @@ def test_c4_bidirectional_gated_full_row(gpu, orc):
     assert np.array_equal(to_np(gl.q), ol.q)
     assert np.array_equal(to_np(gl.k), ol.k)
     got = to_np(gl.out)
-    assert np.isfinite(got).all()
-    err = float(np.abs(got - ol.block(0)).max())
-    _say(f"c4 all {w.t} rows: max|d| vs candle-op oracle {err:.3g}")
-    assert err <= BF16_TOL
+    want = ol.block(0)
+    err, rel = errors(got, want)
+    _say(f"c4 all {w.t} rows: max|d| vs candle-op oracle {err:.3g} ({rel:.3g} of max|ref|)")
+    assert_bf16(got, candle=want, what="c4 row")
     for r0 in (0, 1000, 2047, 3333, 4000, 5555, 7000, 8128):
         _check_blocks(gl, ol, [0], BF16_TOL, rows=(r0, 64))
 
@@ -143,6 +152,9 @@ def _d3_check(gpu, orc, w, tol):
          f"readout alone {err_own:.3g}")
     assert got.shape == (w.readout[1],) and np.isfinite(got).all()
     assert err <= tol and err_own <= tol
+    if w.bf16:
+        assert_bf16(got, candle=want, what=f"{w.name} d3 logits")
+        assert_bf16(got, candle=own, what=f"{w.name} d3 logits, readout alone")
     return err
 
 
@@ -234,9 +246,14 @@ def test_small_packed_passes(gpu, orc, case):
     kall = np.concatenate([kc, kn.transpose(1, 0, 2)], axis=1)
     vall = np.concatenate([vc, vn.transpose(1, 0, 2)], axis=1)
     want = orc.attend(q.transpose(1, 0, 2), kall, vall, ep["mask"], bf)[0].transpose(1, 0, 2)
-    err = float(np.abs(got - want).max())
-    _say(f"  max|d| {err:.3g}")
-    assert err <= (BF16_TOL if bf else F32_TOL)
+    want64 = orc.attend_f64(q.transpose(1, 0, 2), kall, vall, ep["mask"])[0].transpose(1, 0, 2)
+    err, rel = errors(got, want)
+    _say(f"  max|d| {err:.3g} ({rel:.3g} of max|ref|)")
+    if bf:
+        assert_bf16(got, candle=want, exact=want64, what=f"small case {case}")
+    else:
+        assert_f32(got, want, f"small case {case}")
+        assert_f32(got, want64, f"small case {case} vs f64")
 
 
 @pytest.mark.parametrize("shape", ["ramp", "spike", "low", "unseen_first"])
@@ -284,9 +301,10 @@ def test_softmax_max_moves(gpu, orc, shape, max_splits):
         err, err64 = float(np.abs(got - want).max()), float(np.abs(got - want64).max())
         _say(f"{shape} bf16={bf} d={d} splits={max_splits}: max|d| {err:.3g} (f64 {err64:.3g}), max|out| {np.abs(want).max():.3g}")
         if bf:
-            assert err64 <= BF16_TOL
+            assert_bf16(got, exact=want64, what=f"{shape} d={d}")
         else:
-            assert err <= F32_TOL and err64 <= F32_TOL
+            assert_f32(got, want, f"{shape} d={d}")
+            assert_f32(got, want64, f"{shape} d={d} vs f64")
 
 
 def test_packed_equals_each_block_alone_on_gpu(gpu):
@@ -426,7 +444,7 @@ def test_bidirectional_padded_rows(gpu, orc):
     for r in range(len(lengths)):
         sl = slice(r * t, (r + 1) * t)
         want = orc.attend(q[sl].transpose(1, 0, 2), k[sl].transpose(1, 0, 2), v[sl].transpose(1, 0, 2), mask[r], bf)[0]
-        assert np.abs(got[sl] - want.transpose(1, 0, 2)).max() <= BF16_TOL
+        assert_bf16(got[sl], candle=want.transpose(1, 0, 2), what=f"padded row {r} (length {lengths[r]})")
 
 
 def test_kernel_repeats_bitwise(gpu):
@@ -495,8 +513,8 @@ def test_million_key_prefix_many_parts(gpu):
         pr = np.exp(sc - sc.max())
         ref = (pr @ v_all[:keys]) / pr.sum()
         worst = max(worst, float(np.abs(out[i, h] - ref).max()))
+        assert_bf16(out[i, h], exact=ref, what=f"row {i} head {h}")
     _say(f"  parts {attn.plan.n_splits}, max|d| vs exact f64 {worst:.3g}")
-    assert worst <= BF16_TOL
 
 
 def test_long_prefix_many_parts_d256(gpu):
@@ -534,8 +552,8 @@ def test_long_prefix_many_parts_d256(gpu):
         pr = np.exp(sc - sc.max())
         ref = (pr @ v_all) / pr.sum()
         worst = max(worst, float(np.abs(out[i, h] - ref).max()))
+        assert_bf16(out[i, h], exact=ref, what=f"row {i} head {h}")
     _say(f"  parts {attn.plan.n_splits}, max|d| vs exact f64 {worst:.3g}, split vs whole {np.abs(whole - out).max():.3g}")
-    assert worst <= BF16_TOL
 
 
 def test_split_f32_matches_unsplit(gpu):

@@ -185,6 +185,54 @@ def test_gdn_c5_heads_vs_oracle(gpu, orc):
     assert ey <= BF16_TOL
 
 
+def _bf16_close(got, ref):
+    """Each bf16 output within the 2e-2 bar plus one bf16 ulp of its own
+    magnitude (2^-7 |ref|): y is rounded to bf16 once at the end, so a value
+    near a rounding boundary may land one ulp apart, and over 4096 tokens y
+    reaches magnitudes where one ulp exceeds 2e-2."""
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return bool(np.all(np.abs(got - ref) <= BF16_TOL + 2.0 ** -7 * np.abs(ref)))
+
+
+def test_gdn_c5_prefill_then_rows_vs_oracle(gpu, orc):
+    """Config 5's GDN half end to end at its own shape (hybrid.rs:554-617):
+    the 4096-token prefill (Hk 16 -> Hv 32) against the oracle in full (y,
+    conv tail and recurrent state), then 32 rows of 64 tokens that continue
+    from that prefilled state (LayerState::broadcast, decoder.rs:74-88; the
+    GPU reads one state through batch stride 0) against the oracle's rows
+    continuing from its own prefill."""
+    import torch
+    w = configs.c5_gdn()
+    inp = w.inputs()
+    _say(f"test gdn c5 prefill: T={w.t} nk={w.nk} nv={w.nv}")
+    y, co, so = _run_gpu(w, inp, gpu)
+    ry, rco, rso = _run_oracle(orc, w, inp)
+    ey = float(np.abs(to_np(y) - ry).max())
+    es = float(np.abs(to_np(so) - rso).max())
+    _say(f"  prefill: max|d| y {ey:.3g} (max|y| {np.abs(ry).max():.3g}), state {es:.3g} (max|S| {np.abs(rso).max():.3g})")
+    assert np.array_equal(to_np(co), rco)
+    assert es <= F32_TOL
+    assert _bf16_close(to_np(y), ry)
+    rows = configs.c5_gdn_rows()
+    rinp = rows.inputs()
+    _say(f"test gdn c5 rows: {rows.batch} x {rows.t} after the prefill")
+    yr, cor, sor = _run_gpu(rows, rinp, gpu, conv_in=co.expand(rows.batch, -1, -1), s_in=so.expand(rows.batch, -1, -1, -1))
+    ryr, rcor, rsor = _run_oracle(orc, rows, rinp, conv_in=np.repeat(rco, rows.batch, 0), s_in=np.repeat(rso, rows.batch, 0))
+    ey = float(np.abs(to_np(yr) - ryr).max())
+    es = float(np.abs(to_np(sor) - rsor).max())
+    _say(f"  rows: max|d| y {ey:.3g} (max|y| {np.abs(ryr).max():.3g}), state {es:.3g}")
+    assert np.array_equal(to_np(cor), rcor)
+    assert np.isfinite(to_np(yr)).all()
+    assert es <= F32_TOL
+    assert _bf16_close(to_np(yr), ryr)
+    # the rows' GPU result from the oracle's prefilled state too: what is
+    # left of the difference is the rows' own arithmetic
+    yr2, _, sor2 = _run_gpu(rows, rinp, gpu, conv_in=to_dev(rco, True, gpu).expand(rows.batch, -1, -1),
+                            s_in=torch.from_numpy(rso).to(gpu).expand(rows.batch, -1, -1, -1))
+    assert float(np.abs(to_np(sor2) - rsor).max()) <= F32_TOL
+    assert _bf16_close(to_np(yr2), ryr)
+
+
 def test_gdn_c5_split_sequence(gpu):
     """4096 tokens at once == 2048 + 2048 with the carried conv and recurrent
     state (size-independent continuation property at the full 4096-token, 32-head size)."""

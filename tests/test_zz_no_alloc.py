@@ -24,10 +24,11 @@ def _ptr(t):
     return None if t is None else C.c_void_p(t.data_ptr())
 
 
-def _case(gpu, prefix, t, hq, hkv, d, seed):
+def _case(gpu, prefix, t, hq, hkv, d, seed, dtype=None):
     import torch
+    dtype = torch.bfloat16 if dtype is None else dtype
     g = torch.Generator(device="cpu").manual_seed(seed)
-    rnd = lambda *s: torch.randn(*s, generator=g).to(torch.bfloat16).to(gpu)  # noqa: E731
+    rnd = lambda *s: torch.randn(*s, generator=g).to(dtype).to(gpu)  # noqa: E731
     q, kn, vn = rnd(t, hq, d), rnd(t, hkv, d), rnd(t, hkv, d)
     kc, vc = rnd(hkv, prefix, d), rnd(hkv, prefix, d)
     tab = cev_hip.BlockTable.from_rows(1, t, prefix, causal=True)
@@ -43,14 +44,22 @@ def _noalloc(op, q, kn, vn, kc, vc, out):
                                                    _ptr(q), _ptr(kc), _ptr(vc), _ptr(kn), _ptr(vn), None, _ptr(out), stream)
 
 
+# (dtype, head dim, GQA shape, [(prefix, tokens, seed), ...]): every record
+# layout of the split kernels (bf16 d = 128, bf16 d = 256, f32 d = 128),
+# each as two calls in a row, the second smaller than the first
+CASES = [("bf16", 128, (32, 8), [(32768, 16, 1), (4096, 16, 2)]),
+         ("bf16", 256, (16, 4), [(16384, 16, 3), (2048, 16, 4)]),
+         ("f32", 128, (16, 8), [(8192, 16, 5), (1024, 16, 6)])]
+
+
 @pytest.mark.gpu
-def test_noalloc_matches_workspace_entry_on_two_calls(gpu):
+@pytest.mark.parametrize("dtype,d,heads,calls", CASES, ids=[f"{c[0]}-d{c[1]}" for c in CASES])
+def test_noalloc_matches_workspace_entry_on_two_calls(gpu, dtype, d, heads, calls):
     import torch
-    # the 32k-prefix x 16-token shape (split into parts whose records use
-    # the scratch), then a smaller 4k-prefix x 16-token call
-    for prefix, t, seed in ((32768, 16, 1), (4096, 16, 2)):
-        op, (q, kn, vn, kc, vc) = _case(gpu, prefix, t, 32, 8, 128, seed)
-        _say(f"noalloc: prefix {prefix} x {t} tokens, {op.plan.n_splits} parts, {op.plan.workspace_bytes} record bytes")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    for prefix, t, seed in calls:
+        op, (q, kn, vn, kc, vc) = _case(gpu, prefix, t, heads[0], heads[1], d, seed, tdt)
+        _say(f"noalloc {dtype} d={d}: prefix {prefix} x {t} tokens, {op.plan.n_splits} parts, {op.plan.workspace_bytes} record bytes")
         assert op.plan.n_splits > 1 and 0 < op.plan.workspace_bytes <= _abi.CEV_ATTN_SCRATCH_BYTES
         want = op(q, kn, vn, kc, vc)
         got = torch.full_like(q, float("nan"))
@@ -58,6 +67,36 @@ def test_noalloc_matches_workspace_entry_on_two_calls(gpu):
         torch.cuda.synchronize()
         assert torch.isfinite(got.float()).all()
         assert torch.equal(got, want)
+
+
+@pytest.mark.gpu
+def test_noalloc_replays_from_a_graph(gpu):
+    """One direct call (which resolves the scratch address), then the call
+    captured in a HIP graph: every replay, with eager work and
+    synchronisations in between, equals the workspace entry point bit for
+    bit."""
+    import torch
+    op, (q, kn, vn, kc, vc) = _case(gpu, 32768, 16, 32, 8, 128, 7)
+    want = op(q, kn, vn, kc, vc)
+    got = torch.full_like(q, float("nan"))
+    _abi.check(_noalloc(op, q, kn, vn, kc, vc, got))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = _noalloc(op, q, kn, vn, kc, vc, got)
+    assert rc == 0
+    small, (q2, kn2, vn2, kc2, vc2) = _case(gpu, 4096, 16, 32, 8, 128, 8)
+    out2 = torch.empty_like(q2)
+    for i in range(3):
+        got.fill_(float("nan"))
+        if i == 1:  # eager calls in between: the workspace entry point, and a direct call that rewrites the scratch
+            op(q, kn, vn, kc, vc)
+            _abi.check(_noalloc(small, q2, kn2, vn2, kc2, vc2, out2))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i}"
 
 
 def test_noalloc_rejects_plans_beyond_the_scratch(cev):
