@@ -440,7 +440,7 @@ extern "C" int32_t cev_attn_workspace_size(const void* plan_host, size_t* bytes)
   CEV_CHECK_ARG(plan_host != nullptr && bytes != nullptr, "cev_attn_workspace_size: null argument");
   const cev_plan_header* h = (const cev_plan_header*)plan_host;
   CEV_CHECK_ARG(h->magic == CEV_PLAN_MAGIC && h->version == CEV_PLAN_VERSION, "cev_attn_workspace_size: not a plan");
-  *bytes = h->n_splits > 1 ? (size_t)h->t * h->n_q_heads * h->n_splits * cev_attn_partial_floats(h->head_dim) * sizeof(float) : 0;
+  *bytes = h->n_splits > 1 ? (size_t)h->t * h->n_q_heads * h->n_splits * cev_attn_record_bytes(h->dtype, h->head_dim) : 0;
   return CEV_OK;
 }
 

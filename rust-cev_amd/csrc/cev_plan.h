@@ -64,9 +64,13 @@ CEV_HD static inline int cev_attn_tile_rows(int g) { return 32 * kAttnWaves / g;
 CEV_HD static inline int cev_attn_block_n(int dtype, int head_dim) { return (dtype == 1 && head_dim == 128) ? 64 : 32; }
 
 // Per-(row, head, part) partial record in the split workspace: the
-// unnormalised output (head_dim floats), then the running max m (log2
-// units) and the sum l, padded to keep records 16-byte aligned.
-CEV_HD static inline int64_t cev_attn_partial_floats(int head_dim) { return (int64_t)head_dim + 4; }
+// unnormalised output (head_dim values: bf16 for bf16 models, f32 for f32
+// models), then the running max m (log2 units) and the sum l as f32, padded
+// to keep records 16-byte aligned.  The merge rounds its result to the
+// model dtype, so a bf16 model's partial output loses nothing it keeps.
+CEV_HD static inline int64_t cev_attn_record_bytes(int dtype, int head_dim) {
+  return dtype == 1 ? 2 * (int64_t)head_dim + 16 : 4 * ((int64_t)head_dim + 4);
+}
 
 // Split policy.  One attention workgroup fills a CU (its LDS and 8 waves of
 // >128 VGPRs), so a launch runs in rounds of 256 workgroups on MI355X.  The

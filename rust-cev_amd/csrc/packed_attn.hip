@@ -42,7 +42,7 @@ struct AttnArgs {
   const void* vn;
   const void* gate;
   void* out;
-  float* ws;
+  char* ws;  // split records (cev_attn_record_bytes each)
   const int32_t* plan;
   int64_t q_st, q_sh, kc_ss, kc_sh, vc_ss, vc_sh, kn_st, kn_sh, vn_st, vn_sh, g_st, g_sh, o_st, o_sh;
   int32_t n_tiles, t, s_cache, hq, hkv, g, has_gate, n_splits, tile_rows;
@@ -293,6 +293,35 @@ template <>
 __device__ __forceinline__ void load_vec4<float>(const float* p, float* v) {
   const f32x4 g = *(const f32x4*)p;
   for (int e = 0; e < 4; ++e) v[e] = g[e];
+}
+
+// Four values of a record's output as loaded (bf16x4 or f32x4) and their
+// f32 form.
+template <typename T>
+using VecOf = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
+__device__ __forceinline__ f32x4 to_f32x4(const bf16x4& v) { return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}; }
+__device__ __forceinline__ f32x4 to_f32x4(const f32x4& v) { return v; }
+
+// Record of (row, head, part) in the split workspace.
+template <typename T, int D>
+__device__ __forceinline__ char* record(const AttnArgs& a, int row, int head, int part) {
+  return a.ws + (((int64_t)row * a.hq + head) * a.n_splits + part) * cev_attn_record_bytes(sizeof(T) == 2 ? 1 : 0, D);
+}
+
+// Writes this lane's share of a partial record: output values d .. d+3 of
+// every (dt, q4) slice (d = 32 dt + 8 q4 + 4u), then m and l from the
+// lane with u == 0.
+template <typename T, int D>
+__device__ __forceinline__ void write_record(char* rec, const f32x16* o, int u, float m, float l) {
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = dt * 32 + 8 * q4 + 4 * u;
+      const float v[4] = {o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
+      store_vec4<T>((T*)rec + d, v);
+    }
+  if (u == 0) *(f32x4*)(rec + D * sizeof(T)) = f32x4{m, l, 0.0f, 0.0f};
 }
 
 // Word 3 of a raw buffer resource on gfx9: 32-bit data format, no swizzle.
@@ -931,17 +960,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   if (!sr.ok) return;
   const int ue = sr.u;
   if (a.n_splits > 1) {
-    // Partial record: O unnormalised, then m and l.
-    float* rec = a.ws + (((int64_t)sr.row * a.hq + sr.head) * a.n_splits + part) * cev_attn_partial_floats(D);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = dt * 32 + 8 * q4 + 4 * ue;
-        *(f32x4*)(rec + d) = f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
-      }
-    // a row that saw no key (l = 0) records the finite m of an empty part
-    if (ue == 0) *(f32x4*)(rec + D) = f32x4{l > 0.0f ? m_run : -1e30f, l, 0.0f, 0.0f};
+    // Partial record: O unnormalised, then m and l; a row that saw no key
+    // (l = 0) records the finite m of an empty part.
+    write_record<T, D>(record<T, D>(a, sr.row, sr.head, part), o, ue, l > 0.0f ? m_run : -1e30f, l);
     return;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -1128,15 +1149,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
   if (!row_ok) return;
   if (a.n_splits > 1) {
     // Partial record: O unnormalised, then m and l.
-    float* rec = a.ws + (((int64_t)row * a.hq + head) * a.n_splits + part) * cev_attn_partial_floats(D);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = dt * 32 + 8 * q4 + 4 * u;
-        *(f32x4*)(rec + d) = f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
-      }
-    if (u == 0) *(f32x4*)(rec + D) = f32x4{m_run, l, 0.0f, 0.0f};
+    write_record<T, D>(record<T, D>(a, row, head, part), o, u, m_run, l);
     return;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -1455,15 +1468,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
   const float l = pair_sum(l_run);
   if (!row_ok) return;
   if (a.n_splits > 1) {
-    float* rec = a.ws + (((int64_t)row * a.hq + head) * a.n_splits + part) * cev_attn_partial_floats(D);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = dt * 32 + 8 * q4 + 4 * u;
-        *(f32x4*)(rec + d) = f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
-      }
-    if (u == 0) *(f32x4*)(rec + D) = f32x4{m_run, l, 0.0f, 0.0f};
+    write_record<T, D>(record<T, D>(a, row, head, part), o, u, m_run, l);
     return;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -1521,10 +1526,10 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
   const int r = grp * kMergeWaves + wave;
   if ((r >= td.y) | (td.x + r >= a.t)) return;
   const int row = td.x + r;
-  const int64_t pf = cev_attn_partial_floats(D);
+  const int64_t rb = cev_attn_record_bytes(BF ? 1 : 0, D);
   const int S = a.n_splits;
   const int col = lane % Q, phase = lane / Q;
-  const float* rec = a.ws + ((int64_t)row * a.hq + head) * S * pf;
+  const char* rec = record<T, D>(a, row, head, 0);
   // The gate chunk loads with the first records (from a record when there
   // is no gate, and is then unused), not after the merge.
   const int d = 4 * col;
@@ -1537,18 +1542,23 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
   float M = -INFINITY, L = 0.0f;
   f32x4 acc = {};
   for (int s0 = 0; s0 < S; s0 += PS * NB) {
-    f32x4 o[NB];
+    // Every load of the batch is issued before any is used: parts past S
+    // read part S - 1 again and are dropped by the selects below (no
+    // per-part branch, so no wait between the loads).
+    VecOf<T> raw[NB];
     float2 ml[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const int s = s0 + PS * i + phase;
-      if (s < S) {
-        o[i] = *(const f32x4*)(rec + s * pf + 4 * col);
-        ml[i] = *(const float2*)(rec + s * pf + D);
-      } else {
-        o[i] = f32x4{};
-        ml[i] = make_float2(-INFINITY, 0.0f);
-      }
+      const int s = min(s0 + PS * i + phase, S - 1);
+      raw[i] = *(const VecOf<T>*)((const T*)(rec + s * rb) + 4 * col);
+      ml[i] = *(const float2*)(rec + s * rb + D * sizeof(T));
+    }
+    f32x4 o[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const bool ok = s0 + PS * i + phase < S;
+      o[i] = ok ? to_f32x4(raw[i]) : f32x4{};
+      if (!ok) ml[i] = make_float2(-INFINITY, 0.0f);
     }
     float mb = -INFINITY;
 #pragma unroll
@@ -1667,7 +1677,7 @@ int32_t packed_attention_impl(const cev_attn_desc* d, const void* plan_host, con
   a.vn = v_new;
   a.gate = gate;
   a.out = out;
-  a.ws = (float*)workspace;
+  a.ws = (char*)workspace;
   a.plan = (const int32_t*)plan_dev;
   a.q_st = d->q_stride_t;
   a.q_sh = d->q_stride_h;
