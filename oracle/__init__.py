@@ -72,6 +72,7 @@ def _declare(L):
         "orc_branch_mask": (v, [i, i, _f32p]),
         "orc_bidirectional_mask": (v, [i, _i32p, i, _f32p]),
         "orc_attend": (v, [_f32p, _f32p, _f32p, _f32p, i, i, i, i, i, i, i64, i64, i64, i, i, i, _f32p]),
+        "orc_attend_blocked": (v, [_f32p, _f32p, _f32p, _f32p, i, i, i, i, i, i, i64, i64, i64, i, i, i, _f32p]),
         "orc_attend_f64": (v, [_f32p, _f32p, _f32p, _f32p, i, i, i, i, i, i, i64, i64, i64, i, i, _f64p]),
         "orc_sigmoid_gate": (v, [_f32p, _f32p, i64, i]),
         "orc_l2norm": (v, [_f32p, i64, i, _f32p]),
@@ -234,6 +235,29 @@ def attend(q, k, v, mask, bf16: bool, rows=None) -> np.ndarray:
     out = np.full((b, hq, t, d), np.nan, np.float32)
     lib().orc_attend(q.reshape(-1), k.reshape(-1), v.reshape(-1), mask.reshape(-1), b, hq, hkv, t, s, d, q_bs, kv_bs, m_bs,
                      int(bf16), int(row0), int(nrows), out.reshape(-1))
+    return out
+
+
+def attend_blocked(q, k, v, mask, bf16: bool, rows=None) -> np.ndarray:
+    """attend's op sequence with register-blocked FMA products over a packed
+    K^T (oracle/cpu_attend.c): the CPU baseline's timed path.  Same shapes and
+    result layout as attend; d a multiple of 32."""
+    q, k, mask = _attend_shapes(_c(q), _c(k), _c(mask))
+    v = _c(v)
+    if v.ndim == 3:
+        v = v[None]
+    b = max(q.shape[0], k.shape[0], mask.shape[0])
+    hq, t, d = q.shape[1:]
+    hkv, s = k.shape[1], k.shape[2]
+    assert mask.shape[-2:] == (t, s) and d % 32 == 0
+    if q.shape[0] != b:
+        q = np.ascontiguousarray(np.broadcast_to(q, (b,) + q.shape[1:]))
+    kv_bs = 0 if k.shape[0] == 1 else hkv * s * d
+    m_bs = 0 if mask.shape[0] == 1 else t * s
+    row0, nrows = (0, t) if rows is None else rows
+    out = np.full((b, hq, t, d), np.nan, np.float32)
+    lib().orc_attend_blocked(q.reshape(-1), k.reshape(-1), v.reshape(-1), mask.reshape(-1), b, hq, hkv, t, s, d, hq * t * d, kv_bs,
+                             m_bs, int(bf16), int(row0), int(nrows), out.reshape(-1))
     return out
 
 

@@ -265,6 +265,30 @@ def test_attend_f32_matches_f64_textbook(orc):
     assert np.abs(ab - bb).max() < 2e-2
 
 
+@pytest.mark.parametrize("bf16,hq,hkv,t,s,d,batch", [(True, 8, 2, 40, 300, 128, 1), (False, 4, 4, 33, 101, 128, 1),
+                                                       (True, 4, 1, 17, 1003, 256, 1), (True, 8, 2, 9, 70, 128, 3)])
+def test_attend_blocked_matches_attend(orc, bf16, hq, hkv, t, s, d, batch):
+    """The CPU baseline's blocked restatement computes the same candle op
+    sequence: equal to attend up to f32 summation order (f32 models) and one
+    bf16 ulp of a probability or output (bf16 models), over causal masks,
+    GQA, both head dims and a batch of rows sharing one K/V (stride 0)."""
+    rng = np.random.default_rng(11)
+    rnd = (lambda x: orc.round_bf16(x)) if bf16 else (lambda x: x)
+    q = rnd(rng.standard_normal((batch, hq, t, d)).astype(np.float32))
+    k = orc.round_bf16(rng.standard_normal((1, hkv, s, d)).astype(np.float32))
+    v = orc.round_bf16(rng.standard_normal((1, hkv, s, d)).astype(np.float32))
+    m = orc.branch_mask(t, s - t)
+    want = orc.attend(q, k, v, m, bf16)
+    got = orc.attend_blocked(q, k, v, m, bf16)
+    assert np.isfinite(got).all()
+    # bf16: a probability or an output one bf16 ulp apart moves an output by
+    # at most about 2^-8 of the largest one
+    tol = 2.0 ** -8 * float(np.abs(want).max()) if bf16 else 1e-5
+    assert float(np.abs(got - want).max()) <= tol
+    got_rows = orc.attend_blocked(q, k, v, m, bf16, rows=(3, 5))
+    assert np.array_equal(got_rows[:, :, 3:8], got[:, :, 3:8]) and np.isnan(got_rows[:, :, :3]).all()
+
+
 def test_attend_bidirectional_key_permutation(orc):
     t, d = 9, 32
     lengths = [9, 6]
