@@ -1270,12 +1270,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
   const int4* rows = (const int4*)(a.plan + ph.rows_off);
   // Query slot (wave, n) holds row slot / g of the tile, query head slot % g;
   // a wave with no valid row skips the MFMA work and still fetches its rows.
-  const int slot = wave * 32 + n;
-  const int gi = slot % a.g;
-  const int head = kvh * a.g + gi;
-  const int rit = slot / a.g;
-  const bool row_ok = rit < td.y && td.x + rit < a.t;
-  const int row = row_ok ? td.x + rit : 0;
+  const SlotRow sr0 = slot_row(lane, wave, kvh, a.g, td.x, td.y, a.t);
+  const bool row_ok = sr0.ok;
+  const int row = sr0.row, head = sr0.head;
   const bool wave_active = (wave * 32) / a.g < td.y;
   const float c = a.scale_log2;
 
@@ -1466,19 +1463,23 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
   }
 
   const float l = pair_sum(l_run);
-  if (!row_ok) return;
+  // The slot's row and head again, from a lane id the compiler cannot
+  // match with the one above, so they are not kept (spilled) across the loop.
+  const SlotRow sr = slot_row(fresh_lane_id(), wave, kvh, a.g, td.x, td.y, a.t);
+  if (!sr.ok) return;
+  const int ue = sr.u;
   if (a.n_splits > 1) {
-    write_record<T, D>(record<T, D>(a, row, head, part), o, u, m_run, l);
+    write_record<T, D>(record<T, D>(a, sr.row, sr.head, part), o, ue, m_run, l);
     return;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
-  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh : nullptr;
+  T* op = (T*)a.out + (int64_t)sr.row * a.o_st + (int64_t)sr.head * a.o_sh;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)sr.row * a.g_st + (int64_t)sr.head * a.g_sh : nullptr;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = dt * 32 + 8 * q4 + 4 * u;
+      const int d = dt * 32 + 8 * q4 + 4 * ue;
       float v[4], gv[4];
       if (gp) load_vec4<T>(gp + d, gv);
 #pragma unroll
