@@ -554,62 +554,76 @@ __device__ __forceinline__ void wait_b128(i32x4& r) {
 }
 
 // Issue order of the LDS reads of one sub-tile body (NQK = 8 QK units, then
-// NPV = 8 PV units).  QK unit u waits for K read u, then issues K read
-// u + kKPF (if any) and, in its last kVPF units, the two reads of V fragment
-// u - (8 - kVPF).  PV unit j waits for V fragment j, then issues V fragment
-// j + kVPF (if any) and, in its last kKPF units, K read j - (8 - kKPF) of the
-// next body.  The wait of each unit is the number of LDS reads issued after
-// the one it needs; the count below replays one steady-state body.
-// Four or five K fragments ahead measured within 0.5 % of three.
-constexpr int kKPF = 3;  // K fragments in flight ahead of their MFMA
-constexpr int kVPF = 3;  // V fragments in flight ahead of their MFMA
-static_assert(kKPF >= 1 && kKPF <= 8 && kVPF >= 1 && kVPF <= 8, "prefetch depths");
+// NPV = 8 PV units), K reads KPF and V fragments VPF ahead of their MFMA.
+// QK unit u waits for K read u, then issues K read u + KPF (if any) and, in
+// its last VPF units, the two reads of V fragment u - (8 - VPF).  PV unit j
+// waits for V fragment j, then issues V fragment j + VPF (if any) and, in
+// its last KPF units, K read j - (8 - KPF) of the next body.  The wait of
+// each unit is the number of LDS reads issued after the one it needs; the
+// count below replays one steady-state body.
 struct ReadSchedule {
   int wait_a[8], wait_b[8];
 };
-constexpr ReadSchedule read_schedule() {
+constexpr ReadSchedule read_schedule(int kpf, int vpf) {
   ReadSchedule r{};
   int kpos[8] = {}, vhi[8] = {};
   int pos = 0;
   // the previous body's PV units: V reads of that body, then this body's
-  // first kKPF K reads
+  // first kpf K reads
   for (int j = 0; j < 8; ++j) {
-    if (j + kVPF < 8) pos += 2;
-    if (j >= 8 - kKPF) kpos[j - (8 - kKPF)] = pos++;
+    if (j + vpf < 8) pos += 2;
+    if (j >= 8 - kpf) kpos[j - (8 - kpf)] = pos++;
   }
   for (int u = 0; u < 8; ++u) {
     r.wait_a[u] = pos - kpos[u] - 1;
-    if (u + kKPF < 8) kpos[u + kKPF] = pos++;
-    if (u >= 8 - kVPF) {
-      vhi[u - (8 - kVPF)] = pos + 1;
+    if (u + kpf < 8) kpos[u + kpf] = pos++;
+    if (u >= 8 - vpf) {
+      vhi[u - (8 - vpf)] = pos + 1;
       pos += 2;
     }
   }
   for (int j = 0; j < 8; ++j) {
     r.wait_b[j] = pos - vhi[j] - 1;
-    if (j + kVPF < 8) {
-      vhi[j + kVPF] = pos + 1;
+    if (j + vpf < 8) {
+      vhi[j + vpf] = pos + 1;
       pos += 2;
     }
-    if (j >= 8 - kKPF) ++pos;
+    if (j >= 8 - kpf) ++pos;
   }
   return r;
 }
-constexpr ReadSchedule kReads = read_schedule();
-constexpr int kWaitA(int st) { return kReads.wait_a[st]; }
-constexpr int kWaitB(int j) { return kReads.wait_b[j]; }
-constexpr bool waits_in_range() {
+constexpr bool waits_in_range(const ReadSchedule& r) {
   for (int i = 0; i < 8; ++i)
-    if (kReads.wait_a[i] < 0 || kReads.wait_a[i] > 15 || kReads.wait_b[i] < 0 || kReads.wait_b[i] > 15) return false;
+    if (r.wait_a[i] < 0 || r.wait_a[i] > 15 || r.wait_b[i] < 0 || r.wait_b[i] > 15) return false;
   return true;
 }
-static_assert(waits_in_range(), "lgkmcnt range");
-static_assert((kWaitA(0) == 2 && kWaitA(5) == 2 && kWaitA(6) == 3 && kWaitA(7) == 4 && kWaitB(0) == 4 &&
-                   kWaitB(4) == 4 && kWaitB(5) == 4 && kWaitB(6) == 3 && kWaitB(7) == 2),
+// The loop's two forms.  Staggered (STAG): waves 4-7 run one region ahead of
+// waves 0-3; on the 32k-key prefill with all 8 waves busy it ran 1.4 %
+// faster than in step, and four K and two V fragments ahead ran 0.5 %
+// faster there than three and three.  In step, three and three: a tile with
+// at most 4 busy waves (a short block, the KV-streaming shape) has nothing
+// to stagger, and there the staggered form's code ran 3 % slower.
+template <bool STAG>
+struct Schedule {
+  static constexpr int KPF = STAG ? 4 : 3;  // K fragments in flight ahead of their MFMA
+  static constexpr int VPF = STAG ? 2 : 3;  // V fragments in flight ahead of their MFMA
+  static_assert(KPF >= 1 && KPF <= 8 && VPF >= 1 && VPF <= 8, "prefetch depths");
+  static constexpr ReadSchedule reads = read_schedule(KPF, VPF);
+  static_assert(waits_in_range(reads), "lgkmcnt range");
+  static constexpr int wait_a(int st) { return reads.wait_a[st]; }
+  static constexpr int wait_b(int j) { return reads.wait_b[j]; }
+};
+static_assert(Schedule<false>::wait_a(0) == 2 && Schedule<false>::wait_a(5) == 2 && Schedule<false>::wait_a(6) == 3 &&
+                  Schedule<false>::wait_a(7) == 4 && Schedule<false>::wait_b(0) == 4 && Schedule<false>::wait_b(4) == 4 &&
+                  Schedule<false>::wait_b(5) == 4 && Schedule<false>::wait_b(6) == 3 && Schedule<false>::wait_b(7) == 2,
               "wait counts at three fragments ahead");
+static_assert(Schedule<true>::wait_a(0) == 5 && Schedule<true>::wait_a(1) == 3 && Schedule<true>::wait_a(5) == 2 &&
+                  Schedule<true>::wait_a(6) == 1 && Schedule<true>::wait_a(7) == 2 && Schedule<true>::wait_b(0) == 2 &&
+                  Schedule<true>::wait_b(5) == 3 && Schedule<true>::wait_b(6) == 4 && Schedule<true>::wait_b(7) == 2,
+              "wait counts at four K and two V fragments ahead");
 }  // namespace pipe
 
-template <typename T, int D>
+template <typename T, int D, bool STAG>
 __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_kernel_pipe(AttnArgs a) {
   using F = Frag<T, D>;
   using P = typename F::P;
@@ -619,6 +633,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   static_assert(sizeof(T) == 2 && D == 128 && BN == 64 && kAttnWaves == 8, "the pipelined loop is sized for bf16, d = 128");
   static_assert(F::NQK == 8 && F::NPV == 8, "unit layout below");
   using namespace pipe;
+  using Sched = Schedule<STAG>;
   __shared__ __align__(16) char lds[2 * kBuf * kTileBytes];
 
   cev_plan_header ph;
@@ -703,7 +718,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
       return VFrag{read_tr<OFF>(va), read_tr<OFF + 8 * kRowBytes>(va)};
     };
     auto v_ready = [](VFrag& f, auto j_c) {
-      wait_tr<kWaitB(decltype(j_c)::value)>(f.lo, f.hi);
+      wait_tr<Sched::wait_b(decltype(j_c)::value)>(f.lo, f.hi);
       const bf16x4 lo = __builtin_bit_cast(bf16x4, f.lo), hi = __builtin_bit_cast(bf16x4, f.hi);
       return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
@@ -713,7 +728,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
       return read_b128<OFF>(lds_base + koff[decltype(st_c)::value]);
     };
     auto k_ready = [](KFrag& r, auto st_c) {
-      wait_b128<kWaitA(decltype(st_c)::value)>(r);
+      wait_b128<Sched::wait_a(decltype(st_c)::value)>(r);
       return __builtin_bit_cast(bf16x8, r);
     };
 
@@ -813,121 +828,138 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
-    KFrag kf[kKPF];
+    constexpr int KPF = Sched::KPF, VPF = Sched::VPF;
+    KFrag kf[KPF];
     if (wave_active) {
-      static_for<kKPF>([&](auto f_c) { kf[decltype(f_c)::value] = k_issue(I0{}, I1{}, f_c); });
+      static_for<KPF>([&](auto f_c) { kf[decltype(f_c)::value] = k_issue(I0{}, I1{}, f_c); });
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 
-    // ---- main loop, software-pipelined over 32-key sub-tiles j:
-    //   scores S(j+1) = K(j+1) . Q^T run on the MFMA unit while the VALU
-    //   turns S(j) into probabilities; then O += V(j)^T . P(j) runs while
-    //   the VALU takes the row max of S(j+1).  The softmax max and the lazy
-    //   rescale are per sub-tile.  Iteration i reads K of chunks i and i+1
-    //   and V of chunk i, fetches chunk i + kAhead into the buffer chunk
-    //   i-1 used, and before its barrier waits for chunk i+2 to land.
+    // ---- main loop, software-pipelined over 32-key sub-tiles j, in two
+    //   regions per sub-tile:
+    //   A: scores S(j+1) = K(j+1) . Q^T on the MFMA unit while the VALU
+    //      turns S(j) into probabilities, then the lazy-max check;
+    //   B: O += V(j)^T . P(j) on the MFMA unit (no VALU work).
+    //   Iteration i reads K of chunks i and i+1 and V of chunk i, fetches
+    //   chunk i + kAhead into the buffer chunk i-1 used, and before its
+    //   barrier waits for chunk i+2 to land.  In the staggered form, waves
+    //   4-7 run one region ahead of waves 0-3 (they take region A of the
+    //   next chunk's first sub-tile before the barrier), so the two waves of
+    //   a SIMD are in opposite regions and one's softmax VALU work runs
+    //   beside the other's P.V MFMAs; both groups still read only chunks i
+    //   and i+1 in iteration i.
+    VFrag vf[VPF];
+    P p;
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    // Region A of sub-tile KT of the chunk in buffer B0.  Each unit ends in
+    // a scheduling fence, so the order is the program order unit by unit:
+    // one MFMA of one stream next to the VALU work of the other, with
+    // operand reads KPF / VPF units ahead of their MFMA.  The part's last
+    // sub-tile also scores a "next" one from a buffer of stale or zero keys,
+    // never used: that keeps O out of a branch (where the compiler copies
+    // all 64 accumulators).  Its last VPF units issue the first V fragments
+    // of region B.
+    auto region_a = [&](auto b0_c, auto kt_c) {
+      constexpr int B0 = decltype(b0_c)::value, kt = decltype(kt_c)::value;
+      constexpr bool last = kt + 1 == NKT;
+      using BN_c = std::integral_constant<int, last ? (B0 + 1) % kBuf : B0>;  // buffer and sub-tile of the next scores
+      using KTN_c = std::integral_constant<int, last ? 0 : kt + 1>;
+      f32x16& s = kt % 2 == 0 ? sa : sb;
+      f32x16& sn = kt % 2 == 0 ? sb : sa;
+      float rs = 0.0f;
+      static_for<F::NQK>([&](auto st_c) {
+        constexpr int st = decltype(st_c)::value;
+        if constexpr (st == 0)
+          sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_ready(kf[0], st_c), fr.q[0], negm, 0, 0, 0);
+        else
+          fr.qk_mfma(k_ready(kf[st % KPF], st_c), st, sn);
+        if constexpr (st + KPF < F::NQK) kf[st % KPF] = k_issue(BN_c{}, KTN_c{}, std::integral_constant<int, st + KPF>{});
+        if constexpr (st >= F::NQK - VPF)
+          vf[st - (F::NQK - VPF)] = v_issue(b0_c, kt_c, std::integral_constant<int, st - (F::NQK - VPF)>{});
+        const float e0 = fast_exp2(s[2 * st]);
+        const float e1 = fast_exp2(s[2 * st + 1]);
+        const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
+        p.h[st / 4][2 * (st % 4)] = pr[0];
+        p.h[st / 4][2 * (st % 4) + 1] = pr[1];
+        rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
+        pin(rs);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // Lazy max: S(j) came out relative to m_run, and its probabilities
+      // stand as long as their row sum stays within kMaxP (O and l are f32).
+      // Otherwise, or for a row with no max yet, the row moves its max (a
+      // set row only when it grew by more than kRescale) and P(j) is made
+      // again.  This branch issues no LDS operation, so the counted waits of
+      // region B still hold.
+      if (__ballot((rs > kMaxP) | !m_set)) {
+        float ml = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ml = fmaxf(ml, s[i]);
+        const float delta = pair_max(ml);
+        const bool move = m_set ? delta > kRescale : delta > -INFINITY;
+        const float dm = move ? delta : 0.0f;
+        const float alpha = m_set ? fast_exp2(-dm) : 1.0f;
+        m_set = m_set | move;
+        m_run += dm;
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+        rs = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            const bf16x2 pr = {(__bf16)fast_exp2(s[8 * h + j] - dm), (__bf16)fast_exp2(s[8 * h + j + 1] - dm)};
+            p.h[h][j] = pr[0];
+            p.h[h][j + 1] = pr[1];
+            rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
+          }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          sn[i] -= dm;
+          negm[i] = -m_run;
+        }
+      }
+      l_run += rs;
+    };
+    // Region B of sub-tile KT of the chunk in buffer B0: P.V, the next
+    // region's first K reads, then the mask of the next scores (has1: the
+    // part has a chunk after this one).
+    auto region_b = [&](auto b0_c, auto kt_c, bool has1) {
+      constexpr int B0 = decltype(b0_c)::value, kt = decltype(kt_c)::value;
+      constexpr bool last = kt + 1 == NKT;
+      f32x16& sn = kt % 2 == 0 ? sb : sa;
+      static_for<F::NPV>([&](auto j_c) {
+        constexpr int j = decltype(j_c)::value;
+        F::pv_mfma(v_ready(vf[j % VPF], j_c), j, p, o);
+        if constexpr (j + VPF < F::NPV) vf[j % VPF] = v_issue(b0_c, kt_c, std::integral_constant<int, j + VPF>{});
+        // the next region A's first K reads: it scores sub-tile kt + 2
+        if constexpr (j >= F::NPV - KPF)
+          kf[j - (F::NPV - KPF)] = k_issue(std::integral_constant<int, (B0 + (kt + 2) / 2) % kBuf>{},
+                                           std::integral_constant<int, (kt + 2) % 2>{},
+                                           std::integral_constant<int, j - (F::NPV - KPF)>{});
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      if (!last || has1) {
+        const Chunk& chn = last ? chs[1] : chs[0];
+        if (needs_mask(chn)) mask_sub(sn, last ? 0 : kt + 1, chn);
+      }
+    };
+    static_assert(NKT == 2, "two sub-tiles per chunk");
+    const bool lead = STAG && wave >= kAttnWaves / 2;
+    if (wave_active && lead) region_a(I0{}, I0{});
     auto step = [&](int ci, auto buf_tag) {
       constexpr int B0 = decltype(buf_tag)::value;  // buffer of chunk ci
-      constexpr int B1 = (B0 + 1) % kBuf;
+      using B1_c = std::integral_constant<int, (B0 + 1) % kBuf>;
       const bool has1 = ci + 1 < nc;
       chs[kAhead] = next_chunk();
       fetch(chs[kAhead], (B0 + kAhead) % kBuf);
       if (wave_active) {
-        static_for<NKT>([&](auto kt_c) {
-          constexpr int kt = decltype(kt_c)::value;
-          f32x16& s = kt % 2 == 0 ? sa : sb;
-          f32x16& sn = kt % 2 == 0 ? sb : sa;
-          constexpr bool last = kt + 1 == NKT;
-          constexpr int bn = last ? B1 : B0;  // buffer and sub-tile of the next scores
-          constexpr int ktn = last ? 0 : kt + 1;
-          float rs = 0.0f;
-          constexpr int KPF = kKPF, VPF = kVPF;
-          // Each unit below ends in a scheduling fence, so the order is the
-          // program order unit by unit: one MFMA of one stream next to the
-          // VALU work of the other, with operand reads KPF / VPF units ahead
-          // of their MFMA.  The part's last sub-tile also scores a "next"
-          // one from a buffer of stale or zero keys, never used: that keeps
-          // O out of a branch (where the compiler copies all 64 accumulators).
-          using BN_c = std::integral_constant<int, bn>;
-          using KTN_c = std::integral_constant<int, ktn>;
-          VFrag vf[VPF];
-          P p;
-          const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-          // Region A: QK(j+1) on the MFMA unit (from negm); exp2(j), P(j) and
-          // its row sum on the VALU, two probabilities per unit.  Its last
-          // VPF units issue the first V fragments of region B.
-          static_for<F::NQK>([&](auto st_c) {
-            constexpr int st = decltype(st_c)::value;
-            if constexpr (st == 0)
-              sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_ready(kf[0], st_c), fr.q[0], negm, 0, 0, 0);
-            else
-              fr.qk_mfma(k_ready(kf[st % KPF], st_c), st, sn);
-            if constexpr (st + KPF < F::NQK) kf[st % KPF] = k_issue(BN_c{}, KTN_c{}, std::integral_constant<int, st + KPF>{});
-            if constexpr (st >= F::NQK - VPF)
-              vf[st - (F::NQK - VPF)] = v_issue(std::integral_constant<int, B0>{}, kt_c, std::integral_constant<int, st - (F::NQK - VPF)>{});
-            const float e0 = fast_exp2(s[2 * st]);
-            const float e1 = fast_exp2(s[2 * st + 1]);
-            const bf16x2 pr = {(__bf16)e0, (__bf16)e1};
-            p.h[st / 4][2 * (st % 4)] = pr[0];
-            p.h[st / 4][2 * (st % 4) + 1] = pr[1];
-            rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
-            pin(rs);
-            __builtin_amdgcn_sched_barrier(0);
-          });
-          // Lazy max: S(j) came out relative to m_run, and its probabilities
-          // stand as long as their row sum stays within kMaxP (O and l are
-          // f32).  Otherwise, or for a row with no max yet, the row moves its
-          // max (a set row only when it grew by more than kRescale) and P(j)
-          // is made again.  This branch issues no LDS operation, so the
-          // counted waits of region B still hold.
-          if (__ballot((rs > kMaxP) | !m_set)) {
-            float ml = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) ml = fmaxf(ml, s[i]);
-            const float delta = pair_max(ml);
-            const bool move = m_set ? delta > kRescale : delta > -INFINITY;
-            const float dm = move ? delta : 0.0f;
-            const float alpha = m_set ? fast_exp2(-dm) : 1.0f;
-            m_set = m_set | move;
-            m_run += dm;
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
-            rs = 0.0f;
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-              for (int j = 0; j < 8; j += 2) {
-                const bf16x2 pr = {(__bf16)fast_exp2(s[8 * h + j] - dm), (__bf16)fast_exp2(s[8 * h + j + 1] - dm)};
-                p.h[h][j] = pr[0];
-                p.h[h][j + 1] = pr[1];
-                rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
-              }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              sn[i] -= dm;
-              negm[i] = -m_run;
-            }
-          }
-          // Region B: PV(j) on the MFMA unit.
-          static_for<F::NPV>([&](auto j_c) {
-            constexpr int j = decltype(j_c)::value;
-            F::pv_mfma(v_ready(vf[j % VPF], j_c), j, p, o);
-            if constexpr (j + VPF < F::NPV)
-              vf[j % VPF] = v_issue(std::integral_constant<int, B0>{}, kt_c, std::integral_constant<int, j + VPF>{});
-            // the next body's first K reads: it scores sub-tile kt + 2
-            if constexpr (j >= F::NPV - KPF)
-              kf[j - (F::NPV - KPF)] = k_issue(std::integral_constant<int, (B0 + (kt + 2) / 2) % kBuf>{},
-                                               std::integral_constant<int, (kt + 2) % 2>{},
-                                               std::integral_constant<int, j - (F::NPV - KPF)>{});
-            __builtin_amdgcn_sched_barrier(0);
-          });
-          l_run += rs;
-          if (!last || has1) {
-            const Chunk& chn = last ? chs[1] : chs[0];
-            if (needs_mask(chn)) mask_sub(sn, ktn, chn);
-          }
-        });
+        if (!lead) region_a(buf_tag, I0{});
+        region_b(buf_tag, I0{}, has1);
+        region_a(buf_tag, I1{});
+        region_b(buf_tag, I1{}, has1);
+        if (lead && has1) region_a(B1_c{}, I0{});
       }
       // Chunk ci+2 (fetched in iteration ci-1) must have landed before the
       // barrier; chunk ci + kAhead may stay in flight.
@@ -1595,12 +1627,14 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
   store_vec4<T>(op, v);
 }
 
+// stagger: the bf16 d = 128 loop's form (attn_kernel_pipe's STAG).
 template <typename T, int D>
-int32_t launch(const AttnArgs& a, hipStream_t stream) {
+int32_t launch(const AttnArgs& a, bool stagger, hipStream_t stream) {
   const int64_t grid = (int64_t)a.n_tiles * a.n_splits * a.hkv;
   if (grid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "grid of %lld workgroups is too large", (long long)grid);
   if constexpr (sizeof(T) == 2 && D == 128)
-    hipLaunchKernelGGL((attn_kernel_pipe<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
+    hipLaunchKernelGGL((stagger ? attn_kernel_pipe<T, D, true> : attn_kernel_pipe<T, D, false>), dim3((unsigned)grid),
+                       dim3(kAttnWaves * 64), 0, stream, a);
   else if constexpr (sizeof(T) == 2 && D == 256)
     hipLaunchKernelGGL((attn_kernel_wide<T, D>), dim3((unsigned)grid), dim3(kAttnWaves * 64), 0, stream, a);
   else
@@ -1707,10 +1741,21 @@ int32_t packed_attention_impl(const cev_attn_desc* d, const void* plan_host, con
   a.plan_sig = (uint32_t)h->sig;
   hipStream_t s = (hipStream_t)stream;
   if (d->dtype == CEV_BF16) {
-    if (d->head_dim == 128) return launch<__bf16, 128>(a, s);
-    return launch<__bf16, 256>(a, s);
+    if (d->head_dim == 128) {
+      // Staggered loop when some tile keeps more than half of the
+      // workgroup's waves busy (more than 4 x 32 query slots).
+      const int32_t* words = (const int32_t*)plan_host;
+      CEV_CHECK_ARG(h->tiles_off >= (int32_t)(sizeof(cev_plan_header) / 4) &&
+                        (int64_t)h->tiles_off + 8 * (int64_t)h->n_tiles <= (int64_t)h->bytes / 4,
+                    "cev_packed_attention: the plan's tile table lies outside the plan");
+      bool stagger = false;
+      for (int32_t i = 0; i < h->n_tiles && !stagger; ++i)
+        stagger = (int64_t)words[h->tiles_off + 8 * (int64_t)i + 1] * g > 32 * kAttnWaves / 2;
+      return launch<__bf16, 128>(a, stagger, s);
+    }
+    return launch<__bf16, 256>(a, false, s);
   }
-  return launch<float, 128>(a, s);
+  return launch<float, 128>(a, false, s);
 }
 
 // Device addresses of `scratch` (below), one per device, looked up once with that
