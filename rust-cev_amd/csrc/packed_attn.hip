@@ -99,7 +99,13 @@ __device__ __forceinline__ float gate_value(float o, float g, bool bf16) {
   if (bf16) {
     float e = bf16_round(expf(-g));
     float den = bf16_round(e + 1.0f);
-    float sg = bf16_round(1.0f / den);
+    // bf16(1 / den) from the hardware reciprocal (1 ulp): den = D 2^p with
+    // D an 8-bit integer, a bf16 rounding midpoint is M 2^q with M an odd
+    // 9-bit integer, and D M is never a power of two, so 1 / den lies at
+    // least 2^-17 (relative) from every midpoint and a 2^-23 error cannot
+    // change its bf16 rounding.  Below 2^-126 (den > 2^126) the reciprocal
+    // is an f32 denormal, which the division still gives exactly.
+    float sg = bf16_round(den < 0x1p126f ? __builtin_amdgcn_rcpf(den) : 1.0f / den);
     return bf16_round(bf16_round(o) * sg);
   }
   return o * (1.0f / (expf(-g) + 1.0f));
@@ -301,6 +307,49 @@ template <typename T>
 using VecOf = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
 __device__ __forceinline__ f32x4 to_f32x4(const bf16x4& v) { return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}; }
 __device__ __forceinline__ f32x4 to_f32x4(const f32x4& v) { return v; }
+
+// The normalised, optionally gated output of one query slot (row, head):
+// lane half ue holds columns 32 dt + 8 q4 + 4 ue .. +3 of o[dt].  bf16
+// layers multiply by 1/l (the result is rounded to bf16), f32 layers divide
+// by l.  The gate's loads are all issued before the first store, so each of
+// the row's output lines is written in one burst; with one load round trip
+// between stores, lines sat half written in L2 and went to HBM twice.
+template <typename T, int D>
+__device__ __forceinline__ void store_output(const AttnArgs& a, int row, int head, int ue, const f32x16* o, float l) {
+  constexpr int NDT = D / 32;
+  constexpr bool BF = sizeof(T) == 2;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
+  auto value = [&](int dt, int i) { return BF ? o[dt][i] * inv : (l > 0.0f ? o[dt][i] / l : 0.0f); };
+  if (a.has_gate) {
+    const T* gp = (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh;
+    VecOf<T> graw[NDT][4];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) graw[dt][q4] = *(const VecOf<T>*)(gp + dt * 32 + 8 * q4 + 4 * ue);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const f32x4 gv = to_f32x4(graw[dt][q4]);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gate_value(value(dt, 4 * q4 + e), gv[e], BF);
+        store_vec4<T>(op + dt * 32 + 8 * q4 + 4 * ue, v);
+      }
+  } else {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = value(dt, 4 * q4 + e);
+        store_vec4<T>(op + dt * 32 + 8 * q4 + 4 * ue, v);
+      }
+  }
+}
 
 // Record of (row, head, part) in the split workspace.
 template <typename T, int D>
@@ -997,24 +1046,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
     write_record<T, D>(record<T, D>(a, sr.row, sr.head, part), o, ue, l > 0.0f ? m_run : -1e30f, l);
     return;
   }
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  T* op = (T*)a.out + (int64_t)sr.row * a.o_st + (int64_t)sr.head * a.o_sh;
-  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)sr.row * a.g_st + (int64_t)sr.head * a.g_sh : nullptr;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = dt * 32 + 8 * q4 + 4 * ue;
-      float v[4], gv[4];
-      if (gp) load_vec4<T>(gp + d, gv);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float x = o[dt][4 * q4 + e] * inv;
-        if (gp) x = gate_value(x, gv[e], true);
-        v[e] = x;
-      }
-      store_vec4<T>(op + d, v);
-    }
+  store_output<T, D>(a, sr.row, sr.head, ue, o, l);
 }
 
 // --------------------------------------------------------------------------
@@ -1024,7 +1056,6 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
 template <typename T, int D>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
   using F = Frag<T, D>;
-  constexpr bool BF = sizeof(T) == 2;
   constexpr int BN = F::BN;
   constexpr int NT = kAttnWaves * 64;
   constexpr int VEC = F::VEC;
@@ -1184,24 +1215,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
     write_record<T, D>(record<T, D>(a, row, head, part), o, u, m_run, l);
     return;
   }
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh;
-  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh : nullptr;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = dt * 32 + 8 * q4 + 4 * u;
-      float v[4], gv[4];
-      if (gp) load_vec4<T>(gp + d, gv);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float x = BF ? o[dt][4 * q4 + e] * inv : (l > 0.0f ? o[dt][4 * q4 + e] / l : 0.0f);
-        if (gp) x = gate_value(x, gv[e], BF);
-        v[e] = x;
-      }
-      store_vec4<T>(op + d, v);
-    }
+  store_output<T, D>(a, row, head, u, o, l);
 }
 
 // --------------------------------------------------------------------------
@@ -1504,24 +1518,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
     write_record<T, D>(record<T, D>(a, sr.row, sr.head, part), o, ue, m_run, l);
     return;
   }
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  T* op = (T*)a.out + (int64_t)sr.row * a.o_st + (int64_t)sr.head * a.o_sh;
-  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)sr.row * a.g_st + (int64_t)sr.head * a.g_sh : nullptr;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = dt * 32 + 8 * q4 + 4 * ue;
-      float v[4], gv[4];
-      if (gp) load_vec4<T>(gp + d, gv);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float x = o[dt][4 * q4 + e] * inv;
-        if (gp) x = gate_value(x, gv[e], true);
-        v[e] = x;
-      }
-      store_vec4<T>(op + d, v);
-    }
+  store_output<T, D>(a, sr.row, sr.head, ue, o, l);
 }
 
 // Combines the parts of split tiles: for each (row, head),
