@@ -63,14 +63,18 @@ CEV_HD static inline int cev_attn_tile_rows(int g) { return 32 * kAttnWaves / g;
 // register budget of the two head dims and of f32).
 CEV_HD static inline int cev_attn_block_n(int dtype, int head_dim) { return (dtype == 1 && head_dim == 128) ? 64 : 32; }
 
-// Per-(row, head, part) partial record in the split workspace: the
-// unnormalised output (head_dim values: bf16 for bf16 models, f32 for f32
-// models), then the running max m (log2 units) and the sum l as f32, padded
-// to keep records 16-byte aligned.  The merge rounds its result to the
-// model dtype, so a bf16 model's partial output loses nothing it keeps.
-CEV_HD static inline int64_t cev_attn_record_bytes(int dtype, int head_dim) {
-  return dtype == 1 ? 2 * (int64_t)head_dim + 16 : 4 * ((int64_t)head_dim + 4);
+// Bytes per (row, head, part) partial record in the split workspace.  The
+// workspace holds two regions, both indexed by (row * n_q_heads + head) *
+// n_splits + part: first every record's unnormalised output (head_dim
+// values: bf16 for bf16 models, f32 for f32 models; 256 or 512 bytes, so
+// each output starts on a 128-byte line and no line is shared by two
+// parts), then every record's running max m (log2 units) and sum l as two
+// f32.  The merge rounds its result to the model dtype, so a bf16 model's
+// partial output loses nothing it keeps.
+CEV_HD static inline int64_t cev_attn_record_out_bytes(int dtype, int head_dim) {
+  return (dtype == 1 ? 2 : 4) * (int64_t)head_dim;
 }
+CEV_HD static inline int64_t cev_attn_record_bytes(int dtype, int head_dim) { return cev_attn_record_out_bytes(dtype, head_dim) + 8; }
 
 // Split policy.  One attention workgroup fills a CU (its LDS and 8 waves of
 // >128 VGPRs), so a launch runs in rounds of 256 workgroups on MI355X.  The

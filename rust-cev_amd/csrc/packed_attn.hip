@@ -42,7 +42,7 @@ struct AttnArgs {
   const void* vn;
   const void* gate;
   void* out;
-  char* ws;  // split records (cev_attn_record_bytes each)
+  char* ws;  // split records: outputs, then (m, l) pairs (cev_plan.h)
   const int32_t* plan;
   int64_t q_st, q_sh, kc_ss, kc_sh, vc_ss, vc_sh, kn_st, kn_sh, vn_st, vn_sh, g_st, g_sh, o_st, o_sh;
   int32_t n_tiles, t, s_cache, hq, hkv, g, has_gate, n_splits, tile_rows;
@@ -351,26 +351,36 @@ __device__ __forceinline__ void store_output(const AttnArgs& a, int row, int hea
   }
 }
 
-// Record of (row, head, part) in the split workspace.
+// Index of record (row, head, part) in the split workspace.
+__device__ __forceinline__ int64_t record_index(const AttnArgs& a, int row, int head, int part) {
+  return ((int64_t)row * a.hq + head) * a.n_splits + part;
+}
+// Output of record i, and the (m, l) region that follows all outputs.
 template <typename T, int D>
-__device__ __forceinline__ char* record(const AttnArgs& a, int row, int head, int part) {
-  return a.ws + (((int64_t)row * a.hq + head) * a.n_splits + part) * cev_attn_record_bytes(sizeof(T) == 2 ? 1 : 0, D);
+__device__ __forceinline__ T* record_out(const AttnArgs& a, int64_t i) {
+  return (T*)a.ws + i * D;
+}
+template <typename T, int D>
+__device__ __forceinline__ float2* record_ml(const AttnArgs& a) {
+  return (float2*)(a.ws + (int64_t)a.t * a.hq * a.n_splits * D * (int64_t)sizeof(T));
 }
 
-// Writes this lane's share of a partial record: output values d .. d+3 of
-// every (dt, q4) slice (d = 32 dt + 8 q4 + 4u), then m and l from the
-// lane with u == 0.
+// Writes this lane's share of partial record (row, head, part): output
+// values d .. d+3 of every (dt, q4) slice (d = 32 dt + 8 q4 + 4u), then m
+// and l from the lane with u == 0.
 template <typename T, int D>
-__device__ __forceinline__ void write_record(char* rec, const f32x16* o, int u, float m, float l) {
+__device__ __forceinline__ void write_record(const AttnArgs& a, int row, int head, int part, const f32x16* o, int u, float m, float l) {
+  const int64_t i = record_index(a, row, head, part);
+  T* rec = record_out<T, D>(a, i);
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d = dt * 32 + 8 * q4 + 4 * u;
       const float v[4] = {o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]};
-      store_vec4<T>((T*)rec + d, v);
+      store_vec4<T>(rec + d, v);
     }
-  if (u == 0) *(f32x4*)(rec + D * sizeof(T)) = f32x4{m, l, 0.0f, 0.0f};
+  if (u == 0) record_ml<T, D>(a)[i] = make_float2(m, l);
 }
 
 // Word 3 of a raw buffer resource on gfx9: 32-bit data format, no swizzle.
@@ -1043,7 +1053,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu
   if (a.n_splits > 1) {
     // Partial record: O unnormalised, then m and l; a row that saw no key
     // (l = 0) records the finite m of an empty part.
-    write_record<T, D>(record<T, D>(a, sr.row, sr.head, part), o, ue, l > 0.0f ? m_run : -1e30f, l);
+    write_record<T, D>(a, sr.row, sr.head, part, o, ue, l > 0.0f ? m_run : -1e30f, l);
     return;
   }
   store_output<T, D>(a, sr.row, sr.head, ue, o, l);
@@ -1212,7 +1222,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_seq(AttnArgs a) {
   if (!row_ok) return;
   if (a.n_splits > 1) {
     // Partial record: O unnormalised, then m and l.
-    write_record<T, D>(record<T, D>(a, row, head, part), o, u, m_run, l);
+    write_record<T, D>(a, row, head, part, o, u, m_run, l);
     return;
   }
   store_output<T, D>(a, row, head, u, o, l);
@@ -1515,7 +1525,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
   if (!sr.ok) return;
   const int ue = sr.u;
   if (a.n_splits > 1) {
-    write_record<T, D>(record<T, D>(a, sr.row, sr.head, part), o, ue, m_run, l);
+    write_record<T, D>(a, sr.row, sr.head, part, o, ue, m_run, l);
     return;
   }
   store_output<T, D>(a, sr.row, sr.head, ue, o, l);
@@ -1556,14 +1566,15 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
   const int r = grp * kMergeWaves + wave;
   if ((r >= td.y) | (td.x + r >= a.t)) return;
   const int row = td.x + r;
-  const int64_t rb = cev_attn_record_bytes(BF ? 1 : 0, D);
   const int S = a.n_splits;
   const int col = lane % Q, phase = lane / Q;
-  const char* rec = record<T, D>(a, row, head, 0);
+  const int64_t i0 = record_index(a, row, head, 0);
+  const T* rec = record_out<T, D>(a, i0);
+  const float2* rml = record_ml<T, D>(a) + i0;
   // The gate chunk loads with the first records (from a record when there
   // is no gate, and is then unused), not after the merge.
   const int d = 4 * col;
-  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh + d : (const T*)rec;
+  const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh + d : rec;
   float gv[4];
   load_vec4<T>(gp, gv);
 
@@ -1580,8 +1591,8 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int s = min(s0 + PS * i + phase, S - 1);
-      raw[i] = *(const VecOf<T>*)((const T*)(rec + s * rb) + 4 * col);
-      ml[i] = *(const float2*)(rec + s * rb + D * sizeof(T));
+      raw[i] = *(const VecOf<T>*)(rec + (int64_t)s * D + 4 * col);
+      ml[i] = rml[s];
     }
     f32x4 o[NB];
 #pragma unroll

@@ -377,9 +377,9 @@ def test_split_policy(cev):
     d = cev_hip.attn_desc(CEV_BF16, 32, 8, 128, 16, 32768)
     p = cev_hip.AttnPlan(d, hbm)
     assert p.n_splits > 1 and p.n_tiles * p.n_splits * 8 >= 256
-    # one record per (row, head, part): bf16 output values, then f32 m and l
-    # padded to 16 bytes
-    assert p.workspace_bytes == 16 * 32 * p.n_splits * (2 * 128 + 16)
+    # one record per (row, head, part): its bf16 output values in the first
+    # region, its f32 m and l in the second
+    assert p.workspace_bytes == 16 * 32 * p.n_splits * (2 * 128 + 8)
     d.max_splits = 1
     assert cev_hip.AttnPlan(d, hbm).n_splits == 1 and cev_hip.AttnPlan(d, hbm).workspace_bytes == 0
     d.max_splits = 3
