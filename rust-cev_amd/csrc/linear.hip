@@ -16,13 +16,16 @@
 // row once; larger products are plain library GEMMs (hipBLASLt), f32
 // accumulation, the result rounded once to the output dtype as candle's
 // matmul does.
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
 #include <cmath>
 #include <map>
 #include <mutex>
+#include <string>
 #include <tuple>
 #include <type_traits>
+#include <vector>
 
 #include "cev_device.h"
 #include "cev_internal.h"
@@ -136,12 +139,17 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
 
 // hipBLASLt state of one cev_blas handle: the library handle and, per
 // problem shape, the matmul descriptor, layouts and the heuristic's algo.
+// al256: x, w and y all 256-byte aligned (the alignment the picks below
+// were measured at); part of the key, so a plan is never reused on less
+// aligned operands than it was made for.
 struct GemmKey {
   int dtype, out_dtype;
   int64_t m, n, k, ldx, ldw, ldy;
   size_t ws;
+  bool al256;
   bool operator<(const GemmKey& o) const {
-    return std::tie(dtype, out_dtype, m, n, k, ldx, ldw, ldy, ws) < std::tie(o.dtype, o.out_dtype, o.m, o.n, o.k, o.ldx, o.ldw, o.ldy, o.ws);
+    return std::tie(dtype, out_dtype, m, n, k, ldx, ldw, ldy, ws, al256) <
+           std::tie(o.dtype, o.out_dtype, o.m, o.n, o.k, o.ldx, o.ldw, o.ldy, o.ws, o.al256);
   }
 };
 struct GemmPlan {
@@ -150,6 +158,52 @@ struct GemmPlan {
   hipblasLtMatmulAlgo_t algo;
   size_t ws = 0;
 };
+
+// Per-shape algorithm picks for bf16 projections of the config-2 pass
+// (Qwen3-1.7B: 3584 pass tokens), measured offline with gemm_probe.cpp
+// (make gemm-probe): the fastest candidate's hipBLASLt solution index and
+// the FNV-1a hash of its kernel name, with the probe's median times of the
+// heuristic's first pick and of the pick, in us.  Indices number the
+// kernels of one loaded hipBLASLt instance: a pick is used only where its
+// index names the same kernel (by hash) in the instance this process
+// loaded.  The entries are ROCm 7.2's hipBLASLt (what a host that does not
+// load torch binds to); in a torch process libcev_hip.so binds to torch's
+// own copy, whose heuristic first picks the probe measured within 2 % of
+// its fastest candidate on these shapes, so it has no entries.
+// The probe ran every candidate on exactly these shapes and layouts
+// (leading dimensions k, k and n, bf16 output, 256-byte aligned operands,
+// the 32 MiB workspace); a pick applies to nothing else.  Before use it
+// must come back from getAlgosFromIndex, name the recorded kernel and pass
+// matmulIsAlgoSupported for the call's layouts with a workspace no larger
+// than the caller's; otherwise the heuristic's first pick stays.  The
+// library never times candidates itself.
+struct GemmPick {
+  int64_t m, n, k;
+  int index;
+  uint64_t name_hash;
+};
+constexpr GemmPick kPicks[] = {
+    {3584, 4096, 2048, 440058, 0x2d1baa9a7bbf205aull},  // q/k/v projection   48.1 -> 45.8
+    {3584, 2048, 2048, 440090, 0x1eb4eec7c4241052ull},  // o_proj             34.6 -> 28.0
+    {3584, 2048, 6144, 440091, 0x58ff78e43625b963ull},  // down               103.6 -> 74.2
+};
+
+uint64_t fnv1a(const std::string& s) {
+  uint64_t h = 1469598103934665603ull;
+  for (unsigned char c : s) {
+    h ^= c;
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+const GemmPick* find_pick(const GemmKey& key) {
+  if (key.dtype != CEV_BF16 || key.out_dtype != CEV_BF16 || !key.al256 || key.ldx != key.k || key.ldw != key.k || key.ldy != key.n)
+    return nullptr;
+  for (const GemmPick& p : kPicks)
+    if (p.m == key.m && p.n == key.n && p.k == key.k) return &p;
+  return nullptr;
+}
 struct Blas {
   hipblasLtHandle_t lt = nullptr;
   std::mutex mu;
@@ -204,9 +258,25 @@ int32_t gemm_plan(Blas& b, const GemmKey& key, GemmPlan** out) {
   }
   p.algo = heur[0].algo;
   p.ws = heur[0].workspaceSize;
+  if (const GemmPick* pk = find_pick(key)) {
+    std::vector<int> idx{pk->index};
+    std::vector<hipblasLtMatmulHeuristicResult_t> res;
+    const float one = 1.0f, zero = 0.0f;
+    size_t need = 0;
+    if (hipblaslt_ext::getAlgosFromIndex(b.lt, idx, res) == HIPBLAS_STATUS_SUCCESS && !res.empty() &&
+        fnv1a(hipblaslt_ext::getKernelNameFromAlgo(b.lt, res[0].algo)) == pk->name_hash &&
+        hipblaslt_ext::matmulIsAlgoSupported(b.lt, p.desc, &one, p.la, p.lb, &zero, p.lc, p.lc, res[0].algo, need) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        need <= key.ws) {
+      p.algo = res[0].algo;
+      p.ws = need;
+    }
+  }
   *out = &(b.plans[key] = p);
   return CEV_OK;
 }
+
+bool aligned256(const void* p) { return ((uintptr_t)p & 255) == 0; }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -293,7 +363,8 @@ extern "C" int32_t cev_linear(cev_blas handle, int32_t dtype, int32_t out_dtype,
   Blas* b = (Blas*)handle;
   std::lock_guard<std::mutex> lock(b->mu);
   GemmPlan* p = nullptr;
-  int32_t rc = gemm_plan(*b, GemmKey{dtype, out_dtype, m, n, k, ldx, ldw, ldy, workspace_bytes}, &p);
+  const bool al256 = aligned256(x) && aligned256(w) && aligned256(y);
+  int32_t rc = gemm_plan(*b, GemmKey{dtype, out_dtype, m, n, k, ldx, ldw, ldy, workspace_bytes, al256}, &p);
   if (rc) return rc;
   const float beta = 0.0f;
   return blas_status(hipblasLtMatmul(b->lt, p->desc, &alpha, w, p->la, x, p->lb, &beta, y, p->lc, y, p->lc, &p->algo, workspace,

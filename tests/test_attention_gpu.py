@@ -190,6 +190,16 @@ def test_linear_shapes_against_numpy(gpu, orc):
         err = float(np.abs(got - want).max() / max(1e-30, np.abs(want).max()))
         _say(f"linear bf16={bf} m={m} n={n} k={k} f32 out={out32}: max rel err {err:.3g}")
         assert err <= (1e-2 if bf and not out32 else 1e-5)
+    # the config-2 projection shapes with an offline-measured algorithm pick
+    # (contiguous operands: the layout the picks apply to), bf16 out
+    for m, n, k in ((3584, 4096, 2048), (3584, 2048, 2048), (3584, 2048, 6144)):
+        x = orc.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+        wt = orc.round_bf16((0.02 * rng.standard_normal((n, k))).astype(np.float32))
+        got = to_np(cev_hip.linear(to_dev(x, True, gpu), to_dev(wt, True, gpu)))
+        want = orc.round_bf16(ref_linear(x, wt, False))
+        err = float(np.abs(got - want).max() / max(1e-30, np.abs(want).max()))
+        _say(f"linear bf16 picked shape m={m} n={n} k={k}: max rel err {err:.3g}")
+        assert err <= 1e-2
     # gather with conversion and an out-of-range id
     tab = torch.randn(10, 16, device=gpu).to(torch.bfloat16)
     ids = torch.tensor([3, 0, 9, 10], dtype=torch.int32, device=gpu)

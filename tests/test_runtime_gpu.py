@@ -41,3 +41,16 @@ def test_buffers_copies_streams_and_events():
         check(L.cev_stream_destroy(s))
         check(L.cev_free(a))
         check(L.cev_free(b))
+
+
+def test_linear_from_a_host_without_torch():
+    """cev_linear on the config-2 projection shapes from a process that has
+    not loaded torch (so the library binds to ROCm's hipBLASLt, where its
+    per-shape picks apply), against f64 products rounded to bf16."""
+    import os
+    import subprocess
+    import sys
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "linear_host_check.py")
+    r = subprocess.run([sys.executable, script], capture_output=True, text=True, timeout=150)
+    print(r.stdout, r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
