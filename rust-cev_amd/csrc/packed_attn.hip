@@ -54,6 +54,7 @@ constexpr float kRescale = 8.0f;
 // Largest sum of a lane's 16 probabilities of one sub-tile that the d = 128
 // loop accepts before it moves the row's max (so p < 2^16 there).
 constexpr float kMaxP = 65536.0f;
+constexpr float kLog2MaxP = 16.0f;  // log2(kMaxP)
 
 // The plan header on the device must be the host plan's (same signature,
 // same launch shape).  A device plan that is not a copy of the validated
@@ -1330,17 +1331,23 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
   const bool row_ok = sr0.ok;
   const int row = sr0.row, head = sr0.head;
   const bool wave_active = (wave * 32) / a.g < td.y;
-  const float c = a.scale_log2;
 
+  // Q arrives scaled by scale * log2 e (scores in base-2 units), and each
+  // chunk's scores start from -m_run: exp2 is the whole softmax step per
+  // score (the d = 128 loop's scheme, attn_kernel_pipe).
   F fr;
   fr.load_q((const T*)a.q + (int64_t)row * a.q_st + (int64_t)head * a.q_sh, row_ok, u);
+  fr.scale_q(a.scale_log2);
   int4 rv = rows[row];
   if (!row_ok) rv = make_int4(0, 0, -1, 0);
 
   f32x16 o[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
-  float m_run = -1e30f, l_run = 0.0f;
+  // m_set: this row has seen a visible key, and m_run is a max it reached
+  // (0 until then); rows that never see one keep l = 0.
+  float m_run = 0.0f, l_run = 0.0f;
+  bool m_set = false;
 
   const int c0 = (int)((int64_t)part * n_chunks / a.n_splits);
   const int c1 = (int)((int64_t)(part + 1) * n_chunks / a.n_splits);
@@ -1440,7 +1447,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
       fetch(chs[kAhead], (B + kAhead) % kBuf);
       const Chunk ch = chs[0];
       if (wave_active) {
-        f32x16 s = {};
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = -m_run;
         static_for<F::NQK>([&](auto st_c) {
           constexpr int st = decltype(st_c)::value;
           pipe::wait_b128<wait_k(st)>(kf[st % kKPF]);
@@ -1461,21 +1470,31 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
             s[i] = vis ? s[i] : -INFINITY;
           }
         }
-        float mx = -INFINITY;
+        // The max moves lazily (the d = 128 loop's scheme, checked on the
+        // scores): P is made relative to m_run as long as no score of the
+        // lane exceeds it by more than log2(kMaxP), so p < kMaxP.  Otherwise,
+        // or for a row with no max yet, the row takes its max (a set row
+        // only when it grew by more than kRescale) and the scores move by it
+        // before P is made.  The check keeps no copy of the scores, so the
+        // loop needs no more registers than with a per-chunk max.
+        float ml = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
-        const float m_cand = pair_max(mx) * c;
-        const bool grow = m_cand > m_run + kRescale;
-        if (__ballot(grow)) {
-          const float m_new = grow ? m_cand : m_run;
-          const float alpha = fast_exp2(m_run - m_new);
-          m_run = m_new;
+        for (int i = 0; i < 16; ++i) ml = fmaxf(ml, s[i]);
+        if (__ballot((ml > kLog2MaxP) | !m_set)) {
+          const float delta = pair_max(ml);
+          const bool move = m_set ? delta > kRescale : delta > -INFINITY;
+          const float dm = move ? delta : 0.0f;
+          const float alpha = m_set ? fast_exp2(-dm) : 1.0f;
+          m_set = m_set | move;
+          m_run += dm;
           l_run *= alpha;
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[i] -= dm;
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = fast_exp2(__builtin_fmaf(s[i], c, -m_run));
+        for (int i = 0; i < 16; ++i) s[i] = fast_exp2(s[i]);
         P p;
         float rs = 0.0f;
         F::make_p(s, p, rs);
@@ -1525,7 +1544,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
   if (!sr.ok) return;
   const int ue = sr.u;
   if (a.n_splits > 1) {
-    write_record<T, D>(a, sr.row, sr.head, part, o, ue, m_run, l);
+    // a row that saw no key (l = 0) records the finite m of an empty part
+    write_record<T, D>(a, sr.row, sr.head, part, o, ue, l > 0.0f ? m_run : -1e30f, l);
     return;
   }
   store_output<T, D>(a, sr.row, sr.head, ue, o, l);
