@@ -227,11 +227,11 @@ def test_config2_full_bf16_vs_golden(gpu):
     """All 28 layers and the full vocab in bf16 (the config's own dtype)
     against the oracle's bf16 fixture: |dp| <= 3e-2, the bar the reference
     holds its own non-f32 runs to (parity_models.rs:42).  The hidden state
-    is reported and held to 10 % of its norm (relative RMS): the device
+    is reported and held to 7 % of its norm (relative RMS): the device
     keeps attention scores in f32 where candle rounds them to bf16, and
     rounds f32 GEMM sums taken in another order, so every layer moves some
     elements by a bf16 step and 28 residual layers accumulate it (about
-    1.4 % at 2 layers, 4.6 % at 28)."""
+    1.4 % at 2 layers; 4.57 % at 28, with |dp| 0.024)."""
     w = configs.c2(True)
     g = np.load(GOLDEN_BF16)
     _say(f"test 28-layer stack bf16: layers={w.n_layers} vocab={w.vocab}")
@@ -241,7 +241,7 @@ def test_config2_full_bf16_vs_golden(gpu):
     rel = float(np.linalg.norm(hid - g["hidden"]) / np.linalg.norm(g["hidden"]))
     scale = float(np.abs(g["hidden"]).max())
     _say(f"  |dp| {dp:.3g}  hidden relative RMS {rel:.3g}, max|dhidden| {dh:.3g} (|hidden| <= {scale:.3g})")
-    assert dp <= BF16_P_TOL and rel <= 0.1
+    assert dp <= BF16_P_TOL and rel <= 0.07
 
 
 @pytest.mark.skipif(not os.path.exists(GOLDEN), reason="tests/golden/c2_f32.npz not generated")
