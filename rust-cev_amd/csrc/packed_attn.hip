@@ -46,6 +46,7 @@ struct AttnArgs {
   const int32_t* plan;
   int64_t q_st, q_sh, kc_ss, kc_sh, vc_ss, vc_sh, kn_st, kn_sh, vn_st, vn_sh, g_st, g_sh, o_st, o_sh;
   int32_t n_tiles, t, s_cache, hq, hkv, g, has_gate, n_splits, tile_rows;
+  int32_t rows_dense;  // the host plan's tiles cover rows [0, t) in order, each row once
   float scale_log2;
   uint32_t plan_sig;  // signature of the host plan this launch was validated with
 };
@@ -64,14 +65,17 @@ constexpr float kLog2MaxP = 16.0f;  // log2(kMaxP)
 // The header is read at once and every field compared (no short-circuit,
 // which would make each field a dependent load).
 // The header stays in h for the offsets the kernel reads next.
-__device__ __forceinline__ bool plan_ok(const AttnArgs& a, cev_plan_header& h) {
-  h = *(const cev_plan_header*)a.plan;
+__device__ __forceinline__ bool header_ok(const AttnArgs& a, const cev_plan_header& h) {
   // the section offsets follow the header in order (this also loads them
   // with the other fields)
   constexpr int32_t kHeaderWords = (int32_t)(sizeof(cev_plan_header) / 4);
   return (h.magic == CEV_PLAN_MAGIC) & ((uint32_t)h.sig == a.plan_sig) & (h.n_tiles == a.n_tiles) & (h.t == a.t) &
          (h.s_cache == a.s_cache) & (h.n_splits == a.n_splits) & (h.tiles_off >= kHeaderWords) & (h.segs_off >= h.tiles_off) &
          (h.rows_off >= h.segs_off);
+}
+__device__ __forceinline__ bool plan_ok(const AttnArgs& a, cev_plan_header& h) {
+  h = *(const cev_plan_header*)a.plan;
+  return header_ok(a, h);
 }
 
 // Workgroup b of the grid writes NaN over output rows [b t / G, (b+1) t / G)
@@ -1559,6 +1563,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
 // any of it is used, so a batch costs one memory latency, and batches
 // combine with an online rescale.  The launcher picks NB from the part
 // count (fewer registers, more waves per SIMD for few parts).
+// When the plan's tiles cover every row once (rows_dense), workgroups map to
+// rows directly and the record and gate loads go out beside the header load:
+// they only touch the workspace and gate extents the launcher checked, and
+// nothing is stored before the header has passed.  Otherwise a workgroup
+// finds its rows through the tile table after the header check.
 constexpr int kMergeWaves = 4;
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -1574,18 +1583,36 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
   constexpr int PS = 64 / Q;  // parts read side by side: 2 at d = 128, 1 at d = 256
   static_assert(Q * PS == 64, "one wave covers the head dim");
   cev_plan_header ph;
-  if (!plan_ok(a, ph)) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // blockIdx -> (tile, row group of kMergeWaves rows, head)
-  const int tile_rows = a.tile_rows;  // validated against the plan at launch
-  const int groups = (tile_rows + kMergeWaves - 1) / kMergeWaves;
   const int head = blockIdx.x % a.hq;
-  const int grp = (blockIdx.x / a.hq) % groups;
-  const int tile = blockIdx.x / (a.hq * groups);
-  const int4 td = ((const int4*)(a.plan + ph.tiles_off))[2 * tile];
-  const int r = grp * kMergeWaves + wave;
-  if ((r >= td.y) | (td.x + r >= a.t)) return;
-  const int row = td.x + r;
+  int row;
+  if (a.rows_dense) {
+    // The header goes through vector loads (a lane offset the compiler
+    // cannot fold), so no wait for a later kernel argument's scalar load
+    // also waits for it.
+    int zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    const int4* hp = (const int4*)a.plan + zero;
+    int4 hw[sizeof(cev_plan_header) / 16];
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(cev_plan_header) / 16); ++i) hw[i] = hp[i];
+    __builtin_memcpy(&ph, hw, sizeof ph);
+    // blockIdx -> (row group of kMergeWaves rows, head)
+    row = (blockIdx.x / a.hq) * kMergeWaves + wave;
+    if (row >= a.t) return;
+  } else {
+    ph = *(const cev_plan_header*)a.plan;
+    if (!header_ok(a, ph)) return;
+    // blockIdx -> (tile, row group of kMergeWaves rows, head)
+    const int tile_rows = a.tile_rows;  // validated against the plan at launch
+    const int groups = (tile_rows + kMergeWaves - 1) / kMergeWaves;
+    const int grp = (blockIdx.x / a.hq) % groups;
+    const int tile = blockIdx.x / (a.hq * groups);
+    const int4 td = ((const int4*)(a.plan + ph.tiles_off))[2 * tile];
+    const int r = grp * kMergeWaves + wave;
+    if ((r >= td.y) | (td.x + r >= a.t)) return;
+    row = td.x + r;
+  }
   const int S = a.n_splits;
   const int col = lane % Q, phase = lane / Q;
   const int64_t i0 = record_index(a, row, head, 0);
@@ -1636,6 +1663,14 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
     }
     M = m_new;
   }
+  if (a.rows_dense) {
+    // The header is checked only now, so its loads and the record loads
+    // are in flight together.  The empty asm keeps the loads and the
+    // combine ahead of the check (a plain branch would let the compiler
+    // sink them behind it).
+    asm volatile("" ::"v"(L), "v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3]), "v"(gv[0]), "v"(gv[1]), "v"(gv[2]), "v"(gv[3]));
+    if (!header_ok(a, ph)) return;
+  }
   if constexpr (PS == 2) {
     // the two part phases of one column group sit 32 lanes apart
     L += __shfl_xor(L, 32, 64);
@@ -1671,7 +1706,7 @@ int32_t launch(const AttnArgs& a, bool stagger, hipStream_t stream) {
   if (e != hipSuccess) return cev_fail(CEV_ERR_HIP, "packed attention launch: %s", hipGetErrorString(e));
   if (a.n_splits > 1) {
     const int groups = (a.tile_rows + kMergeWaves - 1) / kMergeWaves;
-    const int64_t mgrid = (int64_t)a.n_tiles * groups * a.hq;
+    const int64_t mgrid = a.rows_dense ? (int64_t)((a.t + kMergeWaves - 1) / kMergeWaves) * a.hq : (int64_t)a.n_tiles * groups * a.hq;
     if (mgrid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "merge grid too large");
     const int per_lane = (a.n_splits + 64 / (D / 4) - 1) / (64 / (D / 4));  // parts each lane reads
     if (per_lane <= 2)
@@ -1767,15 +1802,23 @@ int32_t packed_attention_impl(const cev_attn_desc* d, const void* plan_host, con
   a.tile_rows = h->tile_rows;
   a.scale_log2 = d->scale * 1.4426950408889634f;
   a.plan_sig = (uint32_t)h->sig;
+  const int32_t* words = (const int32_t*)plan_host;
+  CEV_CHECK_ARG(h->tiles_off >= (int32_t)(sizeof(cev_plan_header) / 4) &&
+                    (int64_t)h->tiles_off + 8 * (int64_t)h->n_tiles <= (int64_t)h->bytes / 4,
+                "cev_packed_attention: the plan's tile table lies outside the plan");
+  // Tiles that cover rows [0, t) in order, each row once, let the merge map
+  // its workgroups straight to rows.
+  int64_t next_row = 0;
+  for (int32_t i = 0; i < h->n_tiles && next_row >= 0; ++i) {
+    const int32_t r0 = words[h->tiles_off + 8 * (int64_t)i], nr = words[h->tiles_off + 8 * (int64_t)i + 1];
+    next_row = (r0 == next_row && nr >= 1 && nr <= h->tile_rows) ? next_row + nr : -1;
+  }
+  a.rows_dense = next_row == d->t ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
   if (d->dtype == CEV_BF16) {
     if (d->head_dim == 128) {
       // Staggered loop when some tile keeps more than half of the
       // workgroup's waves busy (more than 4 x 32 query slots).
-      const int32_t* words = (const int32_t*)plan_host;
-      CEV_CHECK_ARG(h->tiles_off >= (int32_t)(sizeof(cev_plan_header) / 4) &&
-                        (int64_t)h->tiles_off + 8 * (int64_t)h->n_tiles <= (int64_t)h->bytes / 4,
-                    "cev_packed_attention: the plan's tile table lies outside the plan");
       bool stagger = false;
       for (int32_t i = 0; i < h->n_tiles && !stagger; ++i)
         stagger = (int64_t)words[h->tiles_off + 8 * (int64_t)i + 1] * g > 32 * kAttnWaves / 2;
