@@ -440,6 +440,54 @@ def test_rows_outside_every_block_are_untouched(gpu):
     assert not (o[10:30] == 7).all()
 
 
+def test_split_plan_with_rows_outside_every_block(gpu):
+    """A split plan whose tiles skip rows: the merge finds its rows through
+    the tile table.  Covered rows equal the unsplit result, and rows outside
+    every block keep what the output held."""
+    import torch
+    t, hq, hkv, d, s = 48, 32, 8, 128, 32768
+    B = cev_hip.BlockTable.block
+    tab = cev_hip.BlockTable([B(8, 16, s + 8, spans=[(0, s)]), B(40, 4, s + 40, spans=[(0, s)])], t, s)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    rnd = lambda *sh: torch.randn(*sh, generator=g).to(torch.bfloat16).to(gpu)  # noqa: E731
+    q, kn, vn, kc, vc = rnd(t, hq, d), rnd(t, hkv, d), rnd(t, hkv, d), rnd(hkv, s, d), rnd(hkv, s, d)
+    op = cev_hip.PackedAttention(q, kn, tab, k_cache=kc, s_cache=s, v_new=vn, v_cache=vc)
+    assert op.plan.n_splits > 1
+    out = torch.full((t, hq, d), 7.0, device=gpu, dtype=torch.bfloat16)
+    op(q, kn, vn, kc, vc, out=out)
+    whole = cev_hip.packed_attention(q, kn, vn, tab, k_cache=kc, v_cache=vc, max_splits=1)
+    o, w = to_np(out), to_np(whole)
+    covered = np.zeros(t, bool)
+    covered[8:24] = covered[40:44] = True
+    assert (o[~covered] == 7).all()
+    err = np.abs(o[covered] - w[covered]).max()
+    _say(f"split plan with gaps: parts {op.plan.n_splits}, max|split - unsplit| {err:.3g}")
+    assert err <= 1e-2
+
+
+def test_stale_device_plan_split_gives_nan(gpu):
+    """As the stale-plan test above, for split plans: the attention kernel
+    fills the output with NaN and the merge, whose record loads go out
+    before its header check, stores nothing over it."""
+    import torch
+    t, hq, hkv, d, s = 16, 32, 8, 128, 32768
+    B = cev_hip.BlockTable.block
+    tab_a = cev_hip.BlockTable([B(0, 16, s, spans=[(0, s)])], t, s)
+    tab_b = cev_hip.BlockTable([B(0, 16, s, spans=[(0, s - 64)])], t, s)
+    g = torch.Generator(device="cpu").manual_seed(6)
+    rnd = lambda *sh: torch.randn(*sh, generator=g).to(torch.bfloat16).to(gpu)  # noqa: E731
+    q, kn, vn, kc, vc = rnd(t, hq, d), rnd(t, hkv, d), rnd(t, hkv, d), rnd(hkv, s, d), rnd(hkv, s, d)
+    op_a = cev_hip.PackedAttention(q, kn, tab_a, k_cache=kc, s_cache=s, v_new=vn, v_cache=vc)
+    op_b = cev_hip.PackedAttention(q, kn, tab_b, k_cache=kc, s_cache=s, v_new=vn, v_cache=vc)
+    assert op_a.plan.n_splits > 1 and op_a.plan.n_splits == op_b.plan.n_splits
+    assert torch.isfinite(op_a(q, kn, vn, kc, vc).float()).all()
+    op_a.plan.dev = op_b.plan.dev  # host plan A, device plan B
+    out = torch.zeros_like(q)
+    op_a(q, kn, vn, kc, vc, out=out)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
+
+
 def test_bidirectional_padded_rows(gpu, orc):
     bf, t, hq, hkv, d = True, 40, 8, 2, 256
     lengths = [40, 17, 1, 0]
