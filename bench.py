@@ -438,11 +438,32 @@ def bench_stack(args, w, dev):
     print(json.dumps(res), flush=True)
 
 
-def time_layer(layer, steps: int, warmup: int, graph: bool, settle_ms: float = 0.0):
+MALL_EVICT_BYTES = 512 << 20  # twice the 256 MB memory-side cache (MALL) in front of HBM
+
+
+def mall_evictor(dev):
+    """Returns a function that reads a 512 MiB buffer, so that what the
+    previous step left in the 256 MB MALL is evicted with clean lines (a
+    write would leave dirty lines whose write-backs then compete with the
+    next step's reads).  In a pass through many layers each layer's K/V
+    comes cold from HBM; back-to-back steps of one layer would otherwise
+    read part of a 134 MB prefix from the MALL."""
+    import torch
+    buf = torch.ones(MALL_EVICT_BYTES // 8, dtype=torch.int64, device=dev)
+    acc = torch.zeros((), dtype=torch.int64, device=dev)
+
+    def evict():
+        acc.add_(buf.sum())
+    return evict
+
+
+def time_layer(layer, steps: int, warmup: int, graph: bool, settle_ms: float = 0.0, evict=None):
     """Times `steps` steps of one attention layer: K1, K2 and, for a d3
     workload, the readout of the last position, each bracketed by HIP events
-    on the stream they launch on.  Returns (ms per step by the host clock,
-    mean K1 ms, mean K2 ms, mean readout ms or None)."""
+    on the stream they launch on.  With `evict`, it runs before each timed
+    step, outside the events, and the step time is the sum of the parts'
+    event means instead of the host clock.  Returns (ms per step, mean K1 ms,
+    mean K2 ms, mean readout ms or None)."""
     import torch
     parts = [layer.qknorm, layer.attend] + ([layer.read_out] if layer.readout is not None else [])
 
@@ -464,6 +485,8 @@ def time_layer(layer, steps: int, warmup: int, graph: bool, settle_ms: float = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
+        if evict is not None:
+            evict()
         ev[i][0].record()
         for j, f in enumerate(parts):
             f()
@@ -471,20 +494,29 @@ def time_layer(layer, steps: int, warmup: int, graph: bool, settle_ms: float = 0
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / steps
     means = [statistics.mean(e[j].elapsed_time(e[j + 1]) for e in ev) for j in range(len(parts))]
+    if evict is not None:
+        ms_step = sum(means)
     return ms_step, means[0], means[1], (means[2] if len(means) > 2 else None)
 
 
 def hbm_shape_record(dev, steps: int, warmup: int, settle_ms: float):
     """K2 on the long-prefix short-suffix shape (the 32768-key prefix with one
     16-token block), where the kernel streams K/V and HBM bandwidth bounds
-    it: its mean time and the fraction of the 8 TB/s peak."""
+    it: its mean time and the fraction of the 8 TB/s peak, with the MALL
+    evicted before each step (the K/V comes from HBM, as in a pass through
+    many layers), and the same with the MALL left warm by the previous step
+    under "warm_mall"."""
     from cev_hip import configs
     from cev_hip.layer import AttentionLayer
     w = configs.hbm(1)
-    _, k1_ms, k2_ms, _ = time_layer(AttentionLayer(w, dev), steps, warmup, False, settle_ms)
-    gbps = w.alg_bytes() / (k2_ms * 1e-3) / 1e9
+    layer = AttentionLayer(w, dev)
+    _, k1_ms, k2_ms, _ = time_layer(layer, steps, warmup, False, settle_ms, evict=mall_evictor(dev))
+    _, k1w_ms, k2w_ms, _ = time_layer(layer, steps, warmup, False, 0.0)
+    gbps, gbps_w = (w.alg_bytes() / (ms * 1e-3) / 1e9 for ms in (k2_ms, k2w_ms))
     return {"workload": f"{w.name}: {w.notes}", "k1_ms": k1_ms, "k2_ms": k2_ms, "alg_bytes": w.alg_bytes(),
             "achieved_gbps": gbps, "peak_gbps": PEAK_HBM_GBPS, "frac": gbps / PEAK_HBM_GBPS, "settle_ms": settle_ms,
+            "mall": "evicted before each step (a 512 MiB read outside the timed events)",
+            "warm_mall": {"k1_ms": k1w_ms, "k2_ms": k2w_ms, "achieved_gbps": gbps_w, "frac": gbps_w / PEAK_HBM_GBPS},
             "kernel": "attn_kernel_pipe<bf16,128> (split) + attn_merge_kernel"}
 
 
@@ -521,6 +553,10 @@ def main():
     ap.add_argument("--settle-ms", type=float, default=200.0,
                     help="run the step untimed for this long before the warm-up steps, so that timing starts at the "
                          "card's steady clock (0 skips it)")
+    ap.add_argument("--evict-mall", type=int, default=-1,
+                    help="1: read a 512 MiB buffer before each timed step (outside the events) so the step's data "
+                         "comes from HBM, not the 256 MB MALL; 0: leave the MALL as the previous step left it; "
+                         "-1 (default): evict for --workload hbm only (the default line's hbm_shape always reports both)")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: capture each timed call once in a HIP graph and replay it; 0 (default): launch directly (graph launch costs more than it saves here)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -564,7 +600,9 @@ def main():
         return
     w = configs.WORKLOADS[args.workload]()
     layer = AttentionLayer(w, dev)
-    ms_step, k1_ms, k2_ms, k3_ms = time_layer(layer, args.steps, args.warmup, args.graph, args.settle_ms)
+    evict = args.evict_mall == 1 or (args.evict_mall < 0 and args.workload == "hbm")
+    ms_step, k1_ms, k2_ms, k3_ms = time_layer(layer, args.steps, args.warmup, args.graph, args.settle_ms,
+                                              evict=mall_evictor(dev) if evict else None)
 
     dtype = "bf16" if w.bf16 else "f32"
     flops = w.useful_flops()
@@ -591,6 +629,8 @@ def main():
             "suffix_blocks": len(w.blocks), "block_len": w.blocks[0], "query_tokens": w.t,
             "causal": w.causal, "gated": w.gated,
             "launch": "hip graph replay (K1 and K2 each one graph)" if args.graph else "direct launches",
+            "mall": ("evicted before each step (a 512 MiB read outside the timed events; ms_per_step is the sum of "
+                     "the parts' HIP event means)") if evict else "as the previous step left it",
         },
         "tflops": flops / (ms_step * 1e-3) / 1e12,
         "k1_ms": k1_ms,
