@@ -126,6 +126,18 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The larger of x and its value in lane ^ 16 (within each 32-lane half).
+__device__ __forceinline__ float pair16_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// x plus its value in lane ^ 16 (within each 32-lane half).
+__device__ __forceinline__ float pair16_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x4 lds_read_tr(const __bf16* p) {
@@ -310,6 +322,9 @@ __device__ __forceinline__ void load_vec4<float>(const float* p, float* v) {
 // f32 form.
 template <typename T>
 using VecOf = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
+// E values of T as one load or store: bf16x8 for E = 8, else VecOf<T>.
+template <typename T, int E>
+using VecN = typename std::conditional<E == 8, bf16x8, VecOf<T>>::type;
 __device__ __forceinline__ f32x4 to_f32x4(const bf16x4& v) { return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}; }
 __device__ __forceinline__ f32x4 to_f32x4(const f32x4& v) { return v; }
 
@@ -1558,11 +1573,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
 // Combines the parts of split tiles: for each (row, head),
 //   M = max_s m_s,  L = sum_s 2^(m_s - M) l_s,  O = sum_s 2^(m_s - M) O_s / L.
 // One wave per (row, head), kMergeWaves per workgroup.  Lane l reads the
-// four head-dim columns 4 (l % (D/4)) .. of every (64 / (D/4))-th part
-// starting at part l / (D/4); a batch of NB parts per lane is loaded before
-// any of it is used, so a batch costs one memory latency, and batches
-// combine with an online rescale.  The launcher picks NB from the part
-// count (fewer registers, more waves per SIMD for few parts).
+// head-dim columns E (l % Q) .. +E-1 (E values per lane, Q = D / E lanes
+// per record) of every (64 / Q)-th part starting at part l / Q; a batch of
+// NB parts per lane is loaded before any of it is used, so a batch costs one
+// memory latency, and batches combine with an online rescale.  The launcher
+// picks NB from the part count (fewer registers, more waves per SIMD for
+// few parts).
 // When the plan's tiles cover every row once (rows_dense), workgroups map to
 // rows directly and the record and gate loads go out beside the header load:
 // they only touch the workspace and gate extents the launcher checked, and
@@ -1570,18 +1586,36 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel_wide(AttnArgs a) 
 // finds its rows through the tile table after the header check.
 constexpr int kMergeWaves = 4;
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+// Values per lane access: 16 bytes (8 bf16) at d = 128, where a wave reads
+// four parts side by side (the 32k-prefix x 16-token shape's 32 parts: 42.5
+// / 42.9 us against 44.5 / 43.7 us with 8-byte lanes); 4 values otherwise.
+// At d = 256 the 16-byte form put two parts in a wave, read each gate chunk
+// twice and left half the wave idle at the end: c5a's K2 measured 148.0 /
+// 148.3 against 142.5 / 142.9 us.
+template <typename T, int D>
+struct MergeShape {
+  static constexpr int E = (sizeof(T) == 2 && D == 128) ? 8 : 4;
+  static constexpr int Q = D / E;    // lanes per record
+  static constexpr int PS = 64 / Q;  // parts read side by side
+  static_assert(Q * PS == 64, "one wave covers the head dim");
+};
+
+// Max over the PS part phases of a wave (lanes Q = 64 / PS apart); the
+// lanes of one phase hold the same parts, so they agree already.
+template <int PS>
+__device__ __forceinline__ float phase_max(float x) {
+  static_assert(PS == 1 || PS == 2 || PS == 4, "part phases 16 or 32 lanes apart");
+  if constexpr (PS == 4) x = pair16_max(x);
+  if constexpr (PS >= 2) x = pair_max(x);
   return x;
 }
 
 template <typename T, int D, int NB>
 __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a) {
   constexpr bool BF = sizeof(T) == 2;
-  constexpr int Q = D / 4;    // 4-column groups of a record
-  constexpr int PS = 64 / Q;  // parts read side by side: 2 at d = 128, 1 at d = 256
-  static_assert(Q * PS == 64, "one wave covers the head dim");
+  using MS = MergeShape<T, D>;
+  constexpr int E = MS::E, Q = MS::Q, PS = MS::PS;
+  using VE = VecN<T, E>;
   cev_plan_header ph;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int head = blockIdx.x % a.hq;
@@ -1620,45 +1654,45 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
   const float2* rml = record_ml<T, D>(a) + i0;
   // The gate chunk loads with the first records (from a record when there
   // is no gate, and is then unused), not after the merge.
-  const int d = 4 * col;
+  const int d = E * col;
   const T* gp = a.has_gate ? (const T*)a.gate + (int64_t)row * a.g_st + (int64_t)head * a.g_sh + d : rec;
-  float gv[4];
-  load_vec4<T>(gp, gv);
+  const VE graw = *(const VE*)gp;
 
   // Every record holds a finite m (a part with no visible key keeps its
   // initial -1e30 and l = 0), so M is finite after the first batch.
   float M = -INFINITY, L = 0.0f;
-  f32x4 acc = {};
+  float acc[E] = {};
   for (int s0 = 0; s0 < S; s0 += PS * NB) {
     // Every load of the batch is issued before any is used: parts past S
     // read part S - 1 again and are dropped by the selects below (no
     // per-part branch, so no wait between the loads).
-    VecOf<T> raw[NB];
+    VE raw[NB];
     float2 ml[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int s = min(s0 + PS * i + phase, S - 1);
-      raw[i] = *(const VecOf<T>*)(rec + (int64_t)s * D + 4 * col);
+      raw[i] = *(const VE*)(rec + (int64_t)s * D + d);
       ml[i] = rml[s];
     }
-    f32x4 o[NB];
+    bool ok[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const bool ok = s0 + PS * i + phase < S;
-      o[i] = ok ? to_f32x4(raw[i]) : f32x4{};
-      if (!ok) ml[i] = make_float2(-INFINITY, 0.0f);
+      ok[i] = s0 + PS * i + phase < S;
+      if (!ok[i]) ml[i] = make_float2(-INFINITY, 0.0f);
     }
     float mb = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NB; ++i) mb = fmaxf(mb, ml[i].x);
-    const float m_new = fmaxf(M, wave_max(mb));
+    const float m_new = fmaxf(M, phase_max<PS>(mb));
     const float alpha = fast_exp2(M - m_new);
-    acc *= alpha;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] *= alpha;
     L *= alpha;
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const float w = fast_exp2(ml[i].x - m_new);
-      acc += w * o[i];
+      const float w = fast_exp2(ml[i].x - m_new);  // 0 for a dropped part
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] += w * (ok[i] ? (float)raw[i][e] : 0.0f);
       L += w * ml[i].y;
     }
     M = m_new;
@@ -1668,26 +1702,33 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(AttnArgs a
     // are in flight together.  The empty asm keeps the loads and the
     // combine ahead of the check (a plain branch would let the compiler
     // sink them behind it).
-    asm volatile("" ::"v"(L), "v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3]), "v"(gv[0]), "v"(gv[1]), "v"(gv[2]), "v"(gv[3]));
+    asm volatile("" ::"v"(L), "v"(acc[0]), "v"(acc[E - 1]), "v"(graw));
     if (!header_ok(a, ph)) return;
   }
-  if constexpr (PS == 2) {
-    // the two part phases of one column group sit 32 lanes apart
-    L += __shfl_xor(L, 32, 64);
+  // The PS part phases of one column group sit Q lanes apart: sum them
+  // with lane swaps on the VALU (lane ^ 16, then lane ^ 32).
+  static_assert(PS == 1 || PS == 2 || PS == 4, "part phases 16 or 32 lanes apart");
+  if constexpr (PS == 4) {
+    L = pair16_sum(L);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], 32, 64);
-    if (phase != 0) return;
+    for (int e = 0; e < E; ++e) acc[e] = pair16_sum(acc[e]);
   }
+  if constexpr (PS >= 2) {
+    L = pair_sum(L);
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = pair_sum(acc[e]);
+  }
+  if (phase != 0) return;
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   T* op = (T*)a.out + (int64_t)row * a.o_st + (int64_t)head * a.o_sh + d;
-  float v[4];
+  VE v;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < E; ++e) {
     float x = BF ? acc[e] * inv : (L > 0.0f ? acc[e] / L : 0.0f);
-    if (a.has_gate) x = gate_value(x, gv[e], BF);
-    v[e] = x;
+    if (a.has_gate) x = gate_value(x, (float)graw[e], BF);
+    v[e] = (T)x;
   }
-  store_vec4<T>(op, v);
+  *(VE*)op = v;
 }
 
 // stagger: the bf16 d = 128 loop's form (attn_kernel_pipe's STAG).
@@ -1708,8 +1749,11 @@ int32_t launch(const AttnArgs& a, bool stagger, hipStream_t stream) {
     const int groups = (a.tile_rows + kMergeWaves - 1) / kMergeWaves;
     const int64_t mgrid = a.rows_dense ? (int64_t)((a.t + kMergeWaves - 1) / kMergeWaves) * a.hq : (int64_t)a.n_tiles * groups * a.hq;
     if (mgrid > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "merge grid too large");
-    const int per_lane = (a.n_splits + 64 / (D / 4) - 1) / (64 / (D / 4));  // parts each lane reads
-    if (per_lane <= 2)
+    constexpr int PS = MergeShape<T, D>::PS;
+    const int per_lane = (a.n_splits + PS - 1) / PS;  // parts each lane reads
+    if (per_lane <= 1)
+      hipLaunchKernelGGL((attn_merge_kernel<T, D, 1>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
+    else if (per_lane <= 2)
       hipLaunchKernelGGL((attn_merge_kernel<T, D, 2>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
     else if (per_lane <= 4)
       hipLaunchKernelGGL((attn_merge_kernel<T, D, 4>), dim3((unsigned)mgrid), dim3(kMergeWaves * 64), 0, stream, a);
