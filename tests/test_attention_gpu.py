@@ -228,6 +228,10 @@ SMALL = [
     (True, 16, 8, 128, [(20, 50, 20), (64, 64, 64)], [(0, 9), (1, 33), (0, 2), (1, 64)]),
     (True, 32, 8, 128, [(300, 300, 300)], [(0, 48)] * 5),
     (True, 16, 2, 128, [(130, 130, 130)], [(0, 65)]),
+    # every tile starts with a prefix of one chunk or less (a whole and a
+    # partial chunk), then the local keys of two 64-token blocks
+    (True, 16, 8, 128, [(64, 64, 64)], [(0, 64)] * 4),
+    (True, 16, 8, 128, [(40, 40, 40)], [(0, 64)] * 4),
     (True, 16, 4, 256, [(100, 140, 100)], [(0, 17), (0, 64), (0, 3)]),
     (True, 8, 8, 256, [(33, 33, 33)], [(0, 40)]),
     (True, 16, 2, 256, [(0, 5, 0)], [(0, 31)]),
