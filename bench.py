@@ -562,6 +562,11 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the workload, run `steps` device copies of MIB MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes)")
+    ap.add_argument("--kv-data", default="random", choices=["random", "integer", "zero"],
+                    help="diagnostic: the workload's cached prefix K/V as drawn (random, the default and the only "
+                         "setting for reported figures), rounded to integers, or zero.  Same kernels and shapes, less "
+                         "switching in the matrix cores: it shows how much of K2's time the card's power management sets. "
+                         "The CPU baseline is skipped for the other settings")
     ap.add_argument("--calibrate-gemm", type=int, default=0, metavar="N",
                     help="instead of the workload, time torch.matmul bf16 N^3 on random and on zero operands")
     args = ap.parse_args()
@@ -600,6 +605,10 @@ def main():
         return
     w = configs.WORKLOADS[args.workload]()
     layer = AttentionLayer(w, dev)
+    if args.kv_data != "random" and w.prefix:
+        for t in (layer.pk, layer.pv):
+            t.copy_(torch.round(t.float()).to(t.dtype) if args.kv_data == "integer" else torch.zeros_like(t))
+        torch.cuda.synchronize()
     evict = args.evict_mall == 1 or (args.evict_mall < 0 and args.workload == "hbm")
     ms_step, k1_ms, k2_ms, k3_ms = time_layer(layer, args.steps, args.warmup, args.graph, args.settle_ms,
                                               evict=mall_evictor(dev) if evict else None)
@@ -622,7 +631,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dtype,
-        "data": "synthetic (seeded N(0,1) q/k/v and prefix K/V, QK-norm weights 1 + 0.1 N(0,1))",
+        "data": ("synthetic (seeded N(0,1) q/k/v and prefix K/V, QK-norm weights 1 + 0.1 N(0,1))" if args.kv_data == "random"
+                 else f"diagnostic: seeded N(0,1) q/k/v, prefix K/V {'rounded to integers' if args.kv_data == 'integer' else 'zero'}"),
         "config": {
             "workload": f"{w.name}: {w.notes}",
             "hq": w.hq, "hkv": w.hkv, "head_dim": w.d, "prefix": w.prefix,
@@ -648,7 +658,7 @@ def main():
         res["hbm_shape"] = hbm_shape_record(dev, args.steps, args.warmup, args.settle_ms)
     if args.workload == "c3" and args.c4_shape:
         res["c4_shape"] = c4_shape_record(dev, args.steps, args.warmup, args.settle_ms)
-    if args.cpu_baseline:
+    if args.cpu_baseline and args.kv_data == "random":
         res["cpu_baseline"] = cpu_baseline(w, layer.np_inputs)
     print(json.dumps(res), flush=True)
 
