@@ -49,7 +49,14 @@ constexpr int kSC = 68;    // LDS row stride of 64-wide f32 tiles
 //   Kf  [2][l/16][m 16] = 1 / |k_t| and e^(last - cum_t) of token t = 4m + l/16
 // The scan rebuilds Qd = (q * Qf0) * Qf1 and Kd = (k * 1/|k|) * e^(last - cum)
 // with prep's own two roundings, so both layouts give the same bits; the bf16
-// record is 113 KB instead of 144 KB.
+// record is 113 KB instead of 144 KB.  Qb and Kb depend on the key head only:
+// for the many-chunk scan the first value head of each key head's group writes
+// them, and the scans of the group's other value heads read them from that
+// head's record.
+// In's six tiles above the diagonal are zero.  The scan skips their MFMAs,
+// and the many-chunk scan never loads them either, so prep stores them only
+// for the one-chunk scan, which loads every tile at a fixed offset (it is
+// held to 128 registers, and the clamped addresses cost it spills).
 template <bool BF>
 struct RecLayout;
 template <>
@@ -505,6 +512,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
   const int hr = blockIdx.x / g.n_chunks;
   const int h = hr % g.nv, r = hr / g.nv;
   const int kh = h / (g.nv / g.nk);  // value head h reads key head h / (nv/nk) (qwen35.rs:436-442)
+  // bf16 records for the many-chunk scan: only the group's first value head
+  // stores the raw q / k rows (the one-chunk scan reads its own record's)
+  const bool qk_rows = !BF || g.n_chunks == 1 || h % (g.nv / g.nk) == 0;
+  // intra's zero tiles: read only by the one-chunk scan
+  const bool zero_tiles = g.n_chunks == 1;
   const int key_dim = g.nk * kD;
   const int t0 = c * kC;
   const T* cv = (const T*)g.conved + (int64_t)r * g.t * g.conv_dim;
@@ -664,8 +676,9 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
       return L.Ks[i * kSX + c];
   };
   // Records the inversion's idle waves write: q e^cum (Qd) and k e^(last -
-  // cum) (Kd) in their fragment orders (bf16 models: the raw rows and their
-  // factors), and intra's six zero tiles.
+  // cum) (Kd) in their fragment orders (bf16 models: the raw rows, from the
+  // group's first value head only, and every head's factors), and for the
+  // one-chunk scan intra's six zero tiles.
   constexpr int kQdStores = BF ? kC * kD / 8 : kC * kD / 4;  // 16-byte stores per record part
   auto qd_records = [&](int p0, int step) {
     for (int p = p0; p < kQdStores; p += step) {
@@ -723,6 +736,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
       }
     }
   };
+
   auto zero_intra = [&](int p0, int step) {
     for (int p = p0; p < 6 * 64; p += step) {
       const int q = p >> 6;  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
@@ -762,7 +776,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
     for (int k = 0; k < 16; k += 4) x = mma16(L.Tm[(o + fm) * kSC + k + fq], L.iv(o + k + fq, o + fm), x);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.iv(o + 16 + 4 * fq + e, o + fm) = -x[e];
-  } else {
+  } else if (qk_rows) {
     qd_records(tid - 128, 384);
   }
   operands();
@@ -780,8 +794,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.Tm[(16 * ti2 + 4 * fq + e) * kSC + 16 * tj2 + fm] = bc[e];
   } else {
-    kd_records(tid - 256, kQdStores / 2, 256);
-    zero_intra(tid - 256, 256);
+    if (qk_rows) kd_records(tid - 256, kQdStores / 2, 256);
+    if (zero_tiles) zero_intra(tid - 256, 256);
     factor_records(tid - 256);
   }
   __syncthreads();
@@ -791,7 +805,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
       x = mma16(L.Tm[(16 * ti2 + fm) * kSC + k + fq], L.iv(k + fq, 16 * tj2 + fm), x);
 #pragma unroll
     for (int e = 0; e < 4; ++e) L.iv(32 + 16 * ti2 + 4 * fq + e, 16 * tj2 + fm) = -x[e];
-  } else {
+  } else if (qk_rows) {
     kd_records(kQdStores / 2 + tid - 256, kQdStores, 256);
   }
   __syncthreads();
@@ -849,8 +863,10 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(GdnArgs g) {
 //     chunk's output at the start of the next chunk.
 // The A operands come straight from the fragment-ordered record (L2), the
 // B operands (S, v_new) from LDS.  blockIdx -> (item, slice) keeps the 8
-// slices of one head on one XCD (workgroups go round-robin over the 8
-// XCDs), so each head's records are fetched into one L2 only.
+// slices of one head, and in the bf16 many-chunk scan the value heads of one
+// key head, on one XCD (workgroups go round-robin over the 8 XCDs), so each
+// head's records, and the raw q / k rows the group shares, are fetched into
+// one L2 only.
 constexpr int kXcds = 8;
 constexpr int kScanThreads = 512;
 
@@ -893,11 +909,20 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rt = wave & 3, kh = wave >> 2;
   constexpr int nslice = kD / kW;
-  const int b = blockIdx.x;
-  const int item = (b % kXcds) + kXcds * (b / (kXcds * nslice));  // (row, head) index
-  const int sl = (b / kXcds) % nslice;
+  // value heads that share one key head's q / k rows (bf16 records, many-chunk scan)
+  const int grp = BF && kPrefetch ? g.nv / g.nk : 1;
+  // workgroup b runs on XCD b % 8; the groups G = item / grp with G % 8 ==
+  // that XCD take its workgroups, slice fastest, then group member m
+  const int b = blockIdx.x, y = b / kXcds;
+  const int sl = y % nslice, m = (y / nslice) % grp;
+  const int item = ((y / nslice / grp) * kXcds + b % kXcds) * grp + m;  // (row, head) index
   if (item >= g.batch * g.nv) return;
   const int h = item % g.nv, r = item / g.nv;
+  // float offset from this head's record to its group's first head's, which
+  // holds the raw q / k rows for the many-chunk scan.  The one-chunk scan,
+  // held to 128 registers, reads its own record's copy: the second base
+  // address took it from 124 registers to its cap of 128.
+  const int64_t lead_off = kPrefetch ? -(int64_t)m * g.n_chunks * R::Floats : 0;
   const int col0 = sl * kW;
   const int fm = lane & 15, fq = lane >> 4;
 
@@ -907,7 +932,15 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
   const int kc_off = R::Kc + 4 * (rt * 8 * 64 + 4 * kh * 64 + lane);
   const int qd_off = BF ? R::Qd + 8 * ((rt * 2 + kh) * 64 + lane) : R::Qd + 4 * (rt * 8 * 64 + 4 * kh * 64 + lane);
   const int kd_off = BF ? R::Kd + 8 * (wave * 64 + lane) : R::Kd + 4 * (wave * 4 * 64 + lane);
+  // intra blocks kh and kh + 2 of row tile rt.  Blocks above the diagonal
+  // are zero and their MFMAs are skipped; the many-chunk loop reads the
+  // diagonal block in their place (a line the wave pair reads anyway), so
+  // prep need not store them
   const int in_off = R::In + 4 * (rt * 4 * 64 + kh * 64 + lane);
+  // the second block's distance from the first, wave-uniform (kept in an
+  // SGPR, so the per-lane offset stays one register)
+  const int in_d1 = __builtin_amdgcn_readfirstlane(4 * 64 * (min(kh + 2, rt) - kh));
+  const int in_d0 = __builtin_amdgcn_readfirstlane(4 * 64 * (min(kh, rt) - kh));
   const int nv_off = R::Nv + 4 * ((sl * 4 + rt) * 64 + lane);  // read by kh = 0 only
   const int qf_off = R::Qf + 2 * (16 * rt + fm);
   const int kf_off = R::Kf + 2 * lane;
@@ -930,15 +963,15 @@ __device__ __forceinline__ void gdn_scan(const GdnArgs& g) {
   auto fetch_b = [&](const float* rec, Ops& o, int j) {
     if constexpr (BF) {
       if (j < 2) {
-        o.qb[j] = ldb(rec + qd_off + 4 * j);
-        o.kb[j] = ldb(rec + kd_off + 4 * j);
+        o.qb[j] = ldb(rec + lead_off + qd_off + 4 * j);
+        o.kb[j] = ldb(rec + lead_off + kd_off + 4 * j);
       }
       if (j == 2) o.qf = ld2(rec + qf_off);
     } else {
       o.qd[j] = ld4(rec + qd_off + 256 * j);
       o.kd[j] = ld4(rec + kd_off + 256 * j);
     }
-    if (j < 2) o.in[j] = ld4(rec + in_off + 512 * j);
+    if (j < 2) o.in[j] = kPrefetch ? ld4(rec + in_off + (j == 0 ? in_d0 : in_d1)) : ld4(rec + in_off + 512 * j);
   };
   auto fetch = [&](const float* rec, Ops& o) {
 #pragma unroll
@@ -1349,7 +1382,9 @@ extern "C" int32_t cev_gdn_forward(const cev_gdn_desc* d, const void* mixed, con
   while (g.conv_run > 4 && conv_items_of(g.conv_run) < (int64_t)kConvCus * conv_wg) g.conv_run /= 2;
   const int64_t conv_items = conv_items_of(g.conv_run);
   const int64_t recs = (int64_t)g.batch * g.nv * g.n_chunks;
-  const int64_t slices = ((int64_t)g.batch * g.nv + kXcds - 1) / kXcds * kXcds * (kD / kW);
+  // scan grid: (bf16, many chunks) groups of value heads per key head, rounded up to the 8 XCDs, x group size x slices
+  const int64_t grp = d->dtype == CEV_BF16 && g.n_chunks > 1 ? g.nv / g.nk : 1;
+  const int64_t slices = ((int64_t)g.batch * g.nv / grp + kXcds - 1) / kXcds * kXcds * grp * (kD / kW);
   const int64_t norm_items = (int64_t)g.batch * g.t * g.nv;
   if (recs > INT32_MAX || (conv_items + 511) / 512 > INT32_MAX) return cev_fail(CEV_ERR_UNSUPPORTED, "GDN grid too large");
   if (d->dtype == CEV_BF16) {
