@@ -65,6 +65,25 @@ def test_gdn_small_vs_oracle(gpu, orc, bf16, t):
     assert ey <= (BF16_TOL if bf16 else F32_TOL)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("nk,nv", [(2, 2), (1, 4), (1, 8)])
+def test_gdn_head_groups_vs_oracle(gpu, orc, bf16, nk, nv):
+    """Value heads per key head 1, 4 and 8 over several chunks and an odd
+    batch: the bf16 records keep each key head's q / k rows once, in the
+    group's first value head, and the scan maps a group's heads to one XCD."""
+    w = configs.GdnWorkload("gdn-groups", 14, bf16, 3, 200, nk=nk, nv=nv)
+    _say(f"test gdn head groups: bf16={bf16} B={w.batch} T={w.t} nk={nk} nv={nv}")
+    inp = w.inputs()
+    y, co, so = _run_gpu(w, inp, gpu)
+    ry, rco, rso = _run_oracle(orc, w, inp)
+    ey = float(np.abs(to_np(y) - ry).max())
+    es = float(np.abs(to_np(so) - rso).max())
+    _say(f"  max|d| y {ey:.3g}  state {es:.3g}")
+    assert np.array_equal(to_np(co), rco)
+    assert es <= F32_TOL
+    assert ey <= (BF16_TOL if bf16 else F32_TOL)
+
+
 def test_gdn_conv_silu_outside_table(gpu, orc):
     """bf16 conv outputs outside the SiLU table (|v| >= 128 and |v| < 2^-16):
     q/k channels scaled by 400 and by 1e-6, so every token of the q/k waves
